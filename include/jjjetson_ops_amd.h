@@ -1,0 +1,146 @@
+/*
+ * jjjetson_ops_amd.h — C ABI of the MI355X (gfx950) Q4_0 x Q8_1 quantized matmul path.
+ *
+ * Every entry point is plain C: pointers, sizes, an int status. No C++ or torch
+ * types cross this boundary.  `stream` arguments are `hipStream_t` passed as
+ * `void*` (NULL = the legacy default stream).
+ *
+ * Each declaration names the reference interface it replaces
+ * (paths relative to the AshburnLee/JJJetson_Ops tree).
+ *
+ * Wire formats (identical to the reference's structs):
+ *   block_q8_1_mmq (144 B): half2 ds4[4] {d, s} then int8 qs[128]
+ *       (src/cuda/q8_1.cu:14-18, src/cuda/mm_q4_0_q8_1.cu:41-46)
+ *       Superblock (k/128) of token t lives at block index (k/128)*T + t
+ *       (src/cuda/q8_1.cu:84-87).
+ *   block_q4_0 (18 B): half d then uint8 qs[16]; byte j holds element j in its
+ *       low nibble and element j+16 in its high nibble; value = d*(nib-8).
+ *       Row-major [N][K/32] (src/cuda/mm_q4_0_q8_1.cu:35-38,119).
+ *   output y: fp32, y[m*N + n] (src/cuda/mm_q4_0_q8_1.cu:286).
+ */
+#ifndef JJJETSON_OPS_AMD_H
+#define JJJETSON_OPS_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes returned by every int-returning entry point. */
+#define JJO_OK 0
+#define JJO_ERR_INVALID_ARG 1 /* shape / pointer / alignment validation failed */
+#define JJO_ERR_HIP 2         /* a HIP runtime call failed */
+#define JJO_ERR_NO_DEVICE 3   /* no usable gfx950 device */
+
+#define JJO_QK4_0 32
+#define JJO_QK8_1 32
+#define JJO_QK8_1_MMQ 128
+#define JJO_BLOCK_Q4_0_BYTES 18
+#define JJO_BLOCK_Q8_1_MMQ_BYTES 144
+
+/* Text of the last error raised on the calling thread ("" if none). */
+const char *jjo_last_error(void);
+
+/* Library version string. */
+const char *jjo_version(void);
+
+/*
+ * Bytes the Q8_1 output of an activation with dims [K, ne1, ne2, ne3] occupies.
+ * Matches the block indexing of quantize_q8_1_kernel (src/cuda/q8_1.cu:84-86),
+ * including the per-slice stride ne1*4*ceil(K/512) blocks used when ne2*ne3 > 1.
+ * Returns -1 on invalid dims.
+ */
+int64_t q8_1_output_bytes(const int64_t *dims, int ndims);
+
+/*
+ * Host-buffer quantizer.  Replaces `extern "C" void q8_1(float*, uint8_t*,
+ * std::vector<int>&)` at src/cuda/q8_1.cu:148.  `input` is fp32, dim0 fastest,
+ * dims = [K, ne1, ne2, ne3] (ndims 1..4, missing dims are 1).  K must be a
+ * multiple of 32.  Writes q8_1_output_bytes(dims) bytes to `output`.
+ * Synchronous (H2D, kernel, D2H on an internal stream).
+ */
+int q8_1(const float *input, uint8_t *output, const int64_t *dims, int ndims);
+
+/*
+ * Device-pointer quantizer on the caller's stream, no allocation, no copies.
+ * Has no counterpart in the reference (its quantizer only has the host entry
+ * above); it is the device-side quantize that mat_mul_q4_0_q8_1_device's
+ * contract (src/cuda/mm_q4_0_q8_1.cu:384-392) presupposes.  `d_input` must be
+ * 16-byte aligned.
+ */
+int q8_1_device(const float *d_input, void *d_output, const int64_t *dims, int ndims, void *stream);
+
+/*
+ * Host-side unpacking of Q8_1 blocks.  Replaces parse_q8_1_output at
+ * src/cuda/q8_1.cu:197.  qs_out[n*128], scale_out[n*4] = fp32(d),
+ * sum_out[n*4] = fp32(s).  Pure CPU, no device needed.
+ */
+void parse_q8_1_output(const uint8_t *input, int8_t *qs_out, float *scale_out, float *sum_out,
+                       int64_t n_blocks);
+
+/*
+ * Host-buffer matmul.  Replaces `extern "C" void mat_mul_q4_0_q8_1(const void*,
+ * float*, uint8_t*, float*, std::vector<int>&, int, int)` at
+ * src/cuda/mm_q4_0_q8_1.cu:318.  Quantizes `input` ([K, T] fp32, dims as for
+ * q8_1 with T = ne1*ne2*ne3) into `quant_workspace` (host, T*K/128*144 bytes),
+ * then y[T][N] = dequant(W) . dequant(Xq).  Validation as the reference
+ * (dims[0] == ncols_k, ncols_k % 128 == 0), but failures return
+ * JJO_ERR_INVALID_ARG instead of printing.  Synchronous.
+ */
+int mat_mul_q4_0_q8_1(const void *weight_q4_0, const float *input, uint8_t *quant_workspace,
+                      float *output, const int64_t *dims, int ndims, int nrows_out, int ncols_k);
+
+/*
+ * Device-pointer matmul on the caller's stream.  Replaces
+ * mat_mul_q4_0_q8_1_device at src/cuda/mm_q4_0_q8_1.cu:394 (same argument
+ * order: ncols_k, nrows_out, batch).  d_x_q8_1 is in the quantizer's layout
+ * (superblock-major, see above).  Picks the decode GEMV (small batch) or the
+ * int8-MFMA GEMM.  No allocation, asynchronous.
+ */
+int mat_mul_q4_0_q8_1_device(const void *d_w_q4_0, const void *d_x_q8_1, float *d_y, int ncols_k,
+                             int nrows_out, int batch, void *stream);
+
+/* Kernel selector for mat_mul_q4_0_q8_1_device_algo. */
+#define JJO_ALGO_AUTO 0
+#define JJO_ALGO_GEMV_DOT4 1 /* streaming v_dot4 GEMV, batch <= 16 */
+#define JJO_ALGO_MFMA 2      /* int8 MFMA tile GEMM, any batch */
+
+/*
+ * As mat_mul_q4_0_q8_1_device with an explicit kernel choice.  Has no
+ * counterpart in the reference; it exists for parity tests and crossover
+ * tuning of the one entry above.
+ */
+int mat_mul_q4_0_q8_1_device_algo(const void *d_w_q4_0, const void *d_x_q8_1, float *d_y,
+                                  int ncols_k, int nrows_out, int batch, int algo, void *stream);
+
+/*
+ * Test-only: per-block integer dot sums sumi[(m*N + n)*(K/32) + b] =
+ * sum_{j<32} nib_j * q_j with unsigned nibbles (the `sumi` of
+ * q4_0_q8_1_vec_dot_impl, src/cuda/mm_q4_0_q8_1.cu:71-90).  No counterpart
+ * entry in the reference; it exposes the integer stage for bit-exact checks.
+ */
+int mat_mul_q4_0_q8_1_block_sums_device(const void *d_w_q4_0, const void *d_x_q8_1,
+                                        int32_t *d_sumi, int ncols_k, int nrows_out, int batch,
+                                        void *stream);
+
+/*
+ * Grouped (MoE expert) matmul in one launch.  Replaces the per-expert fp32
+ * moe_grouped_gemm_nt calls (src/cuda/moe/moe_pipeline_sota.cu:47-76,181-189)
+ * for the Q4_0 up-projection.  Routes are sorted by expert;
+ * expert_offsets[e]..expert_offsets[e+1] are expert e's routes
+ * (src/cuda/moe/moe_dispatch_sota.cu:63-72).  d_x_q8_1 holds the quantized
+ * routed activations, superblock-major over n_routes "tokens".  Expert e's
+ * weight is d_w_q4_0 + e*nrows_out*(ncols_k/32)*18.  Route r's output row goes
+ * to d_y[route_dst[r]*nrows_out ...] (route_dst may be NULL: identity).
+ */
+int mat_mul_q4_0_q8_1_grouped_device(const void *d_w_q4_0, const void *d_x_q8_1,
+                                     const int32_t *d_expert_offsets, int n_experts,
+                                     const int32_t *d_route_dst, float *d_y, int ncols_k,
+                                     int nrows_out, int n_routes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* JJJETSON_OPS_AMD_H */

@@ -1,0 +1,393 @@
+// Prefill / MoE-expert GEMM of Q4_0 weights x Q8_1 activations on gfx950
+// int8 matrix cores.
+//
+// Math is the reference's per-block epilogue (src/cuda/mm_q4_0_q8_1.cu:71-93,
+// summed over K at :256-269):
+//     y[m][n] = sum_b d_w[n,b] * (sumi[n,m,b] * d_x[m,b] - 8 * s_x[m,b])
+// with sumi the exact unsigned-nibble x int8 dot of one 32-block.
+//
+// MI355X design
+//   * One v_mfma_i32_32x32x32_i8 covers exactly one 32-wide K block, so each
+//     MFMA result is the exact int32 `sumi` tile of one block.
+//   * The MFMA accumulator is seeded with the integer 0x4B400000 (the bits of
+//     the float 1.5*2^23): after the MFMA adds sumi (|sumi| < 2^16) the register
+//     read as fp32 is exactly 1.5*2^23 + sumi.  The epilogue is then two fp32
+//     ops per element and block, with no int->float conversion:
+//         t   = fma(D_as_float, d_x/8, -1.5*2^23 * d_x/8)   (= round(sumi*d_x)/8)
+//         acc = fma(d_w (fp16 via v_fma_mix), t, acc)
+//   * The "-8 * s_x" term, sum_b d_w[n,b] * s_x[m,b], is itself a contraction
+//     over blocks: one v_mfma_f32_32x32x8_f16 per 8 blocks adds
+//     sum_b d_w * (-s_x) into the same accumulator (fp16 x fp16 products are
+//     exact in fp32).  The result is y = 8 * acc (exact power-of-two scale).
+//   * Those two fp32 ops per element-block are the bound of this kernel:
+//     2 VALU lane-ops per 64 int8 MACs+adds.  On MI355X (64 fp32 lanes/clk/CU,
+//     8192 int8 ops/clk/CU) that is 4x the MFMA time, i.e. about 25% of int8
+//     peak at best.
+//   * Workgroup tile 128 (weight rows) x 128 (tokens) x 256 (K per stage);
+//     four waves in 2x2, each owning 2x2 MFMA tiles of 32x32.
+//   * Weights are staged once per workgroup: raw 18-byte blocks (dwordx4
+//     loads), nibbles expanded to int8 in K order while writing LDS, scales
+//     stored twice (fp16 row-major for the f16 MFMA, and permuted so a lane's
+//     16 epilogue rows are one 32-byte run).
+//   * Activations use the quantizer's superblock-major layout: for a fixed
+//     superblock the 128 tokens of a tile are one contiguous 18 KB run, copied
+//     to LDS verbatim with 16-byte loads.
+//   * Next stage's global loads are issued into registers before the current
+//     stage's MFMA/epilogue work (register double buffering).
+#include <hip/hip_fp16.h>
+
+#include "q4q8_common.hpp"
+
+namespace jjo {
+namespace {
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));           // 16-B aligned
+typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x2a4 __attribute__((ext_vector_type(2), aligned(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int BN = 128;          // weight rows per workgroup
+constexpr int BM = 128;          // tokens per workgroup
+constexpr int KB = 8;            // 32-blocks per stage (K = 256)
+constexpr int kThreads = 256;
+
+// LDS carve-up (bytes)
+constexpr int kXsBytes = 2 * BM * kQ8BlockBytes;         // 36864: [2 superblocks][BM][144]
+constexpr int kWqStride = KB * 32 + 16;                  // 272: one row's 8 unpacked blocks + pad
+constexpr int kWqBytes = BN * kWqStride;                 // 34816
+constexpr int kWdEpiBytes = KB * BN * 2;                 // [KB][BN] fp16, rows permuted
+constexpr int kWdRowBytes = BN * KB * 2;                 // [BN][KB] fp16
+constexpr int kOffWq = kXsBytes;
+constexpr int kOffWdEpi = kOffWq + kWqBytes;
+constexpr int kOffWdRow = kOffWdEpi + kWdEpiBytes;
+constexpr int kSmemBytes = kOffWdRow + kWdRowBytes;      // 75776
+
+constexpr uint32_t kBiasBits = 0x4B400000u;              // 1.5 * 2^23
+constexpr float kBias = 12582912.0f;
+
+// Position of tile-local row r (0..31) in the epilogue scale layout: the 16 rows
+// a lane half owns in the 32x32 MFMA output (rows 8q + 4h + i) become contiguous.
+__device__ __forceinline__ int epi_perm(int r) {
+    const int q = r >> 3, h = (r >> 2) & 1, i = r & 3;
+    return h * 16 + q * 4 + i;
+}
+
+struct Staged {
+    uint32_t w[18];   // this thread's 4 raw Q4_0 blocks (72 bytes)
+    u32x4 x[9];       // this thread's 9 x 16 bytes of activation blocks
+};
+
+template <bool kGrouped>
+__global__ __launch_bounds__(kThreads, 1) void gemm_q4_0_q8_1_mfma_kernel(
+    const uint8_t *__restrict__ w_all, const uint8_t *__restrict__ xq, float *__restrict__ y, int K,
+    int N, int M, const int32_t *__restrict__ expert_offsets, int n_experts,
+    const int32_t *__restrict__ route_dst) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint8_t *xs = smem;
+    uint8_t *wq = smem + kOffWq;
+    _Float16 *wd_epi = reinterpret_cast<_Float16 *>(smem + kOffWdEpi);
+    _Float16 *wd_row = reinterpret_cast<_Float16 *>(smem + kOffWdRow);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wn = wave >> 1;  // row half of the workgroup tile
+    const int wm = wave & 1;   // token half
+    const int l32 = lane & 31;
+    const int hh = lane >> 5;  // K half inside an MFMA operand / row group in the output
+
+    const int n0 = blockIdx.x * BN;
+    const size_t row_bytes = (size_t)(K / kQK) * kQ4BlockBytes;
+    const int nb = K / kQK;
+    const int n_chunks = (nb + KB - 1) / KB;
+
+    // ---- token range of this workgroup ----
+    int m0, m_end;
+    const uint8_t *w = w_all;
+    if constexpr (kGrouped) {
+        // Tile t of the concatenated per-expert tile lists.
+        int t = blockIdx.y;
+        int e = 0;
+        m0 = -1;
+        for (; e < n_experts; ++e) {
+            const int beg = expert_offsets[e], end = expert_offsets[e + 1];
+            const int tiles = (end - beg + BM - 1) / BM;
+            if (t < tiles) {
+                m0 = beg + t * BM;
+                m_end = end;
+                break;
+            }
+            t -= tiles;
+        }
+        if (m0 < 0) return;  // uniform over the workgroup
+        w = w_all + (size_t)e * N * row_bytes;
+    } else {
+        m0 = blockIdx.y * BM;
+        m_end = M;
+    }
+
+    // ---- staging helpers ----
+    const int st_row = tid >> 1;    // W: one row, half of the 8 blocks per thread
+    const int st_half = tid & 1;
+    const int st_grow = min(n0 + st_row, N - 1);
+
+    auto issue_loads = [&](Staged &s, int c) {
+        const int blk0 = c * KB + st_half * 4;
+        if (blk0 < nb) {
+            const uint8_t *p = w + (size_t)st_grow * row_bytes + (size_t)blk0 * kQ4BlockBytes;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const u32x4a4 v = *reinterpret_cast<const u32x4a4 *>(p + 16 * i);
+                s.w[4 * i + 0] = v.x; s.w[4 * i + 1] = v.y; s.w[4 * i + 2] = v.z; s.w[4 * i + 3] = v.w;
+            }
+            const u32x2a4 v = *reinterpret_cast<const u32x2a4 *>(p + 64);
+            s.w[16] = v.x; s.w[17] = v.y;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 18; ++i) s.w[i] = 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < 9; ++i) {
+            const int idx = tid + kThreads * i;        // 16-byte unit, 0..2303
+            const int sl = idx >= 1152 ? 1 : 0;
+            const int within = idx - sl * 1152;
+            const int tok = m0 + (within * 16) / kQ8BlockBytes;
+            const int sb = c * 2 + sl;
+            if (tok < m_end && sb * 4 < nb) {
+                const uint8_t *p = xq + ((size_t)sb * M + m0) * kQ8BlockBytes + (size_t)within * 16;
+                s.x[i] = *reinterpret_cast<const u32x4 *>(p);
+            } else {
+                s.x[i] = u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+    };
+
+    auto store_lds = [&](const Staged &s) {
+#pragma unroll
+        for (int i = 0; i < 9; ++i) {
+            const int idx = tid + kThreads * i;
+            *reinterpret_cast<u32x4 *>(xs + idx * 16) = s.x[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // block i of this thread's four: even blocks start dword-aligned, odd ones
+            // start 2 bytes into a dword (their nibbles are then dword-aligned).
+            uint32_t q[4];
+            uint32_t dbits;
+            const int base = 9 * (i >> 1);
+            if ((i & 1) == 0) {
+                dbits = s.w[base] & 0xffffu;
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    q[k] = __builtin_amdgcn_alignbyte(s.w[base + k + 1], s.w[base + k], 2);
+            } else {
+                dbits = s.w[base + 4] >> 16;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) q[k] = s.w[base + 5 + k];
+            }
+            const int b = st_half * 4 + i;
+            u32x4 lo, hi;
+            lo.x = q[0] & 0x0f0f0f0fu; lo.y = q[1] & 0x0f0f0f0fu;
+            lo.z = q[2] & 0x0f0f0f0fu; lo.w = q[3] & 0x0f0f0f0fu;
+            hi.x = (q[0] >> 4) & 0x0f0f0f0fu; hi.y = (q[1] >> 4) & 0x0f0f0f0fu;
+            hi.z = (q[2] >> 4) & 0x0f0f0f0fu; hi.w = (q[3] >> 4) & 0x0f0f0f0fu;
+            uint8_t *dst = wq + st_row * kWqStride + b * 32;
+            *reinterpret_cast<u32x4 *>(dst) = lo;
+            *reinterpret_cast<u32x4 *>(dst + 16) = hi;
+            const unsigned short dh = (unsigned short)dbits;
+            reinterpret_cast<unsigned short *>(wd_epi)[b * BN + (st_row & ~31) + epi_perm(st_row & 31)] = dh;
+            reinterpret_cast<unsigned short *>(wd_row)[st_row * KB + b] = dh;
+        }
+    };
+
+    // ---- accumulators ----
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[rt][ct][v] = 0.0f;
+
+    i32x16 bias;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) bias[v] = (int32_t)kBiasBits;
+
+    Staged st;
+    issue_loads(st, 0);
+
+    for (int c = 0; c < n_chunks; ++c) {
+        __syncthreads();          // previous stage's LDS reads are done
+        store_lds(st);
+        __syncthreads();
+        if (c + 1 < n_chunks) issue_loads(st, c + 1);
+
+        const int kb_here = min(KB, nb - c * KB);  // multiple of 4
+
+        // Activation headers (d, s) of both superblocks for this lane's columns.
+        uint32_t hdr[2][2][4];  // [ct][sl][g]
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+            const int col = wm * 64 + ct * 32 + l32;
+#pragma unroll
+            for (int sl = 0; sl < 2; ++sl) {
+                const u32x4 h = *reinterpret_cast<const u32x4 *>(xs + (sl * BM + col) * kQ8BlockBytes);
+                hdr[ct][sl][0] = h.x; hdr[ct][sl][1] = h.y; hdr[ct][sl][2] = h.z; hdr[ct][sl][3] = h.w;
+            }
+        }
+
+#pragma unroll
+        for (int b = 0; b < KB; ++b) {
+            if (b < kb_here) {
+                const int sl = b >> 2, g = b & 3;
+                i32x4 bop[2], aop[2];
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) {
+                    const int col = wm * 64 + ct * 32 + l32;
+                    bop[ct] = *reinterpret_cast<const i32x4 *>(xs + (sl * BM + col) * kQ8BlockBytes +
+                                                               16 + 32 * g + 16 * hh);
+                }
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    const int row = wn * 64 + rt * 32 + l32;
+                    aop[rt] = *reinterpret_cast<const i32x4 *>(wq + row * kWqStride + b * 32 + 16 * hh);
+                }
+                i32x16 d[2][2];
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                    for (int ct = 0; ct < 2; ++ct)
+                        d[rt][ct] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[rt], bop[ct], bias, 0, 0, 0);
+
+                float dx8[2], nb8[2];
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct) {
+                    const uint32_t ds = hdr[ct][sl][g];
+                    const float dx = __half2float(__ushort_as_half((unsigned short)(ds & 0xffffu)));
+                    dx8[ct] = dx * 0.125f;
+                    nb8[ct] = -kBias * dx8[ct];
+                }
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    const int rbase = (wn * 2 + rt) * 32 + hh * 16;
+                    const u32x4 w0 = *reinterpret_cast<const u32x4 *>(wd_epi + b * BN + rbase);
+                    const u32x4 w1 = *reinterpret_cast<const u32x4 *>(wd_epi + b * BN + rbase + 8);
+                    const uint32_t wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+                    for (int ct = 0; ct < 2; ++ct) {
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) {
+                            const f16x2 pr = __builtin_bit_cast(f16x2, wv[v >> 1]);
+                            const float dwv = (float)((v & 1) ? pr.y : pr.x);
+                            const float t = fmaf(__int_as_float(d[rt][ct][v]), dx8[ct], nb8[ct]);
+                            acc[rt][ct][v] = fmaf(dwv, t, acc[rt][ct][v]);
+                        }
+                    }
+                }
+            }
+        }
+
+        // sum_b d_w * (-s_x) for the (up to) 8 blocks of this stage, on the f16 MFMA.
+        {
+            f16x4 aop[2], bop[2];
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                const int row = wn * 64 + rt * 32 + l32;
+                aop[rt] = *reinterpret_cast<const f16x4 *>(wd_row + row * KB + 4 * hh);
+            }
+            const bool live = c * KB + 4 * hh < nb;
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                const uint32_t *h = hdr[ct][hh];
+                uint32_t lo = (h[0] >> 16) | (h[1] & 0xffff0000u);
+                uint32_t hi = (h[2] >> 16) | (h[3] & 0xffff0000u);
+                lo ^= 0x80008000u;
+                hi ^= 0x80008000u;
+                if (!live) { lo = 0u; hi = 0u; }
+                const u32x2 pk = {lo, hi};
+                bop[ct] = __builtin_bit_cast(f16x4, pk);
+            }
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int ct = 0; ct < 2; ++ct)
+                    acc[rt][ct] = __builtin_amdgcn_mfma_f32_32x32x8f16(aop[rt], bop[ct], acc[rt][ct], 0, 0, 0);
+        }
+    }
+
+    // ---- store: y[m][n] = 8 * acc ----
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+        const int m = m0 + wm * 64 + ct * 32 + l32;
+        if (m >= m_end) continue;
+        int out_row = m;
+        if constexpr (kGrouped) {
+            if (route_dst != nullptr) out_row = route_dst[m];
+        }
+        float *yrow = y + (size_t)out_row * N;
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = n0 + wn * 64 + rt * 32 + 8 * q + 4 * hh;
+                const float v0 = 8.0f * acc[rt][ct][4 * q + 0];
+                const float v1 = 8.0f * acc[rt][ct][4 * q + 1];
+                const float v2 = 8.0f * acc[rt][ct][4 * q + 2];
+                const float v3 = 8.0f * acc[rt][ct][4 * q + 3];
+                if (n + 3 < N && (N & 3) == 0) {
+                    *reinterpret_cast<float4 *>(yrow + n) = make_float4(v0, v1, v2, v3);
+                } else {
+                    if (n + 0 < N) yrow[n + 0] = v0;
+                    if (n + 1 < N) yrow[n + 1] = v1;
+                    if (n + 2 < N) yrow[n + 2] = v2;
+                    if (n + 3 < N) yrow[n + 3] = v3;
+                }
+            }
+        }
+    }
+}
+
+template <bool kGrouped>
+hipError_t set_smem_attr() {
+    static bool done = false;
+    if (!done) {
+        hipError_t e = hipFuncSetAttribute((const void *)gemm_q4_0_q8_1_mfma_kernel<kGrouped>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kSmemBytes);
+        if (e != hipSuccess) return e;
+        done = true;
+    }
+    return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t launch_gemm_mfma(const void *w, const void *xq, float *y, int K, int N, int M,
+                            hipStream_t stream) {
+    hipError_t e = set_smem_attr<false>();
+    if (e != hipSuccess) return e;
+    const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
+    hipLaunchKernelGGL(gemm_q4_0_q8_1_mfma_kernel<false>, grid, dim3(kThreads), kSmemBytes, stream,
+                       (const uint8_t *)w, (const uint8_t *)xq, y, K, N, M, nullptr, 0, nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_mfma_grouped(const void *w, const void *xq, const int32_t *expert_offsets,
+                                    int n_experts, const int32_t *route_dst, float *y, int K,
+                                    int N, int n_routes, hipStream_t stream) {
+    hipError_t e = set_smem_attr<true>();
+    if (e != hipSuccess) return e;
+    // Upper bound on the number of token tiles over all experts.
+    const int max_tiles = (n_routes + BM - 1) / BM + n_experts;
+    const dim3 grid((N + BN - 1) / BN, max_tiles);
+    hipLaunchKernelGGL(gemm_q4_0_q8_1_mfma_kernel<true>, grid, dim3(kThreads), kSmemBytes, stream,
+                       (const uint8_t *)w, (const uint8_t *)xq, y, K, N, n_routes, expert_offsets,
+                       n_experts, route_dst);
+    return hipGetLastError();
+}
+
+}  // namespace jjo

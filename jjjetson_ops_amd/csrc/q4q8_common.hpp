@@ -1,0 +1,47 @@
+// Shared definitions of the gfx950 Q4_0 x Q8_1 path: wire formats, error
+// plumbing and the kernel launchers each translation unit provides.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "jjjetson_ops_amd.h"
+
+namespace jjo {
+
+constexpr int kQK = 32;             // values per Q4_0 block and per Q8_1 group
+constexpr int kQSuper = 128;        // values per block_q8_1_mmq
+constexpr int kQ8BlockBytes = 144;  // sizeof(block_q8_1_mmq)
+constexpr int kQ4BlockBytes = 18;   // sizeof(block_q4_0)
+
+// Set the calling thread's error text (printf-style).  Returns `code`.
+int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+// Clear the calling thread's error text.
+void clear_error();
+// Map a HIP status to JJO_ERR_HIP with a message naming `what`.
+int hip_fail(hipError_t e, const char *what);
+
+#define JJO_HIP_TRY(expr)                                  \
+    do {                                                   \
+        hipError_t jjo_e_ = (expr);                        \
+        if (jjo_e_ != hipSuccess) return ::jjo::hip_fail(jjo_e_, #expr); \
+    } while (0)
+
+// Kernel launchers (asynchronous on `stream`).  Shapes are validated by the
+// C-ABI layer before these are called.
+hipError_t launch_quantize_q8_1(const float *x, void *y, int64_t K, int64_t ne1, int64_t nz,
+                                hipStream_t stream);
+hipError_t launch_gemv_dot4(const void *w, const void *xq, float *y, int K, int N, int M,
+                            hipStream_t stream);
+hipError_t launch_gemm_mfma(const void *w, const void *xq, float *y, int K, int N, int M,
+                            hipStream_t stream);
+hipError_t launch_gemm_mfma_grouped(const void *w, const void *xq, const int32_t *expert_offsets,
+                                    int n_experts, const int32_t *route_dst, float *y, int K,
+                                    int N, int n_routes, hipStream_t stream);
+hipError_t launch_block_sums(const void *w, const void *xq, int32_t *sumi, int K, int N, int M,
+                             hipStream_t stream);
+
+// Largest batch the dot4 GEMV kernel is instantiated for.
+constexpr int kGemvMaxBatch = 8;
+
+}  // namespace jjo

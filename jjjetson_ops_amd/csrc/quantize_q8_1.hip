@@ -1,0 +1,98 @@
+// Q8_1 activation quantizer for gfx950 (wave64).
+//
+// Semantics follow quantize_q8_1_kernel (src/cuda/q8_1.cu:20-104) bit for bit:
+//   * a 32-value group is spread over 8 lanes holding 4 consecutive floats each;
+//   * amax = max |x| and sum = sum x are reduced over those 8 lanes with the
+//     xor-4, xor-2, xor-1 butterfly; the per-lane sum is ((x0+x1)+x2)+x3, so the
+//     group sum is ((t0+t4)+(t2+t6))+((t1+t5)+(t3+t7)) exactly as the reference;
+//   * d_inv = amax > 0 ? 127/amax : 0 (IEEE divide), q = roundf(x*d_inv);
+//   * ds4[g] = half2(1/d_inv, sum), round-to-nearest-even (zero group: d = +inf).
+//
+// MI355X mapping: a 256-thread workgroup covers 1024 consecutive values of one
+// token (8 superblocks); each lane does one 16-byte load, the butterfly uses
+// ds_swizzle inside 32-lane groups (no LDS memory traffic), each half-wave
+// stores one contiguous 128-byte qs run plus four 4-byte ds words.  The kernel
+// is HBM-bound (4 B read + 1.125 B written per value).
+#include <hip/hip_fp16.h>
+
+#include "q4q8_common.hpp"
+
+namespace jjo {
+namespace {
+
+// ds_swizzle bit-mode pattern: and_mask = 0x1f, xor_mask = `x` (within 32 lanes).
+template <int X>
+__device__ __forceinline__ float swz_xor(float v) {
+    constexpr int pattern = 0x1f | (X << 10);
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), pattern));
+}
+
+__device__ __forceinline__ uint32_t pack_q(float v0, float v1, float v2, float v3) {
+    const int32_t a = (int32_t)roundf(v0);
+    const int32_t b = (int32_t)roundf(v1);
+    const int32_t c = (int32_t)roundf(v2);
+    const int32_t d = (int32_t)roundf(v3);
+    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+           ((uint32_t)(d & 0xff) << 24);
+}
+
+__global__ __launch_bounds__(256) void quantize_q8_1_kernel(const float *__restrict__ x,
+                                                            uint8_t *__restrict__ y, int64_t K,
+                                                            int64_t K_pad, int64_t ne1,
+                                                            int64_t slice_blocks) {
+    const int64_t i0 = ((int64_t)blockIdx.y * 256 + threadIdx.x) * 4;  // value index in the token
+    if (i0 >= K_pad) return;  // whole 32-groups leave together (K_pad % 128 == 0)
+    const int64_t m = blockIdx.x;
+    const int64_t z = blockIdx.z;
+
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    const bool live = i0 < K;  // uniform over each 8-lane group since K % 32 == 0
+    if (live) v = *reinterpret_cast<const float4 *>(x + (z * ne1 + m) * K + i0);
+
+    float amax = fmaxf(fabsf(v.x), fmaxf(fabsf(v.y), fmaxf(fabsf(v.z), fabsf(v.w))));
+    float sum = v.x + v.y;
+    sum = sum + v.z;
+    sum = sum + v.w;
+    amax = fmaxf(amax, swz_xor<4>(amax));
+    sum = sum + swz_xor<4>(sum);
+    amax = fmaxf(amax, swz_xor<2>(amax));
+    sum = sum + swz_xor<2>(sum);
+    amax = fmaxf(amax, swz_xor<1>(amax));
+    sum = sum + swz_xor<1>(sum);
+
+    const float d_inv = (amax > 0.0f) ? 127.0f / amax : 0.0f;
+    const uint32_t q = pack_q(v.x * d_inv, v.y * d_inv, v.z * d_inv, v.w * d_inv);
+
+    const int64_t blk = z * slice_blocks + (i0 / kQSuper) * ne1 + m;
+    uint8_t *out = y + blk * kQ8BlockBytes;
+    const int iqs = (int)(i0 % kQSuper);
+    if (live) {
+        *reinterpret_cast<uint32_t *>(out + 16 + iqs) = q;
+        if ((iqs & 31) == 0) {
+            const __half hd = __float2half_rn(1.0f / d_inv);
+            const __half hs = __float2half_rn(sum);
+            const uint32_t ds = (uint32_t)__half_as_ushort(hd) | ((uint32_t)__half_as_ushort(hs) << 16);
+            *reinterpret_cast<uint32_t *>(out + 4 * (iqs / 32)) = ds;
+        }
+    } else {
+        // Groups past K in the last superblock: deterministic zero bytes.
+        *reinterpret_cast<uint32_t *>(out + 16 + iqs) = 0u;
+        if ((iqs & 31) == 0) *reinterpret_cast<uint32_t *>(out + 4 * (iqs / 32)) = 0u;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_quantize_q8_1(const float *x, void *y, int64_t K, int64_t ne1, int64_t nz,
+                                hipStream_t stream) {
+    const int64_t K_pad = (K + kQSuper - 1) / kQSuper * kQSuper;
+    // Per-slice block stride of the reference kernel: ne1 * gridDim.y * 128/32 with
+    // gridDim.y = ceil(K/512) (src/cuda/q8_1.cu:84,173).  Irrelevant when nz == 1.
+    const int64_t slice_blocks = ne1 * 4 * ((K + 511) / 512);
+    const dim3 grid((unsigned)ne1, (unsigned)((K_pad + 1023) / 1024), (unsigned)nz);
+    hipLaunchKernelGGL(quantize_q8_1_kernel, grid, dim3(256), 0, stream, x, (uint8_t *)y, K, K_pad,
+                       ne1, slice_blocks);
+    return hipGetLastError();
+}
+
+}  // namespace jjo
