@@ -5,11 +5,14 @@ K=4096 -> N=11008.  One step = quantize the fp32 activation to Q8_1 on the
 device + the Q4_0 x Q8_1 GEMV, exactly what a decode layer does per linear.
 ``value`` is effective weight GB/s of the whole step (weight bytes / step
 time).  Weight buffers rotate over > 512 MB so the 256 MB MALL cannot serve
-them.  ``roofline`` is the GEMV kernel alone (per-launch HIP events on the
-launch stream).  The other BASELINE configs are measured the same way and
-reported under ``configs``.
+them.  Timed steps are captured in one HIP graph and replayed, bracketed by
+HIP events on the launch stream.  ``roofline`` is the GEMV kernel alone (a
+graph of back-to-back GEMV launches).  The other BASELINE configs are measured
+the same way and reported under ``configs``.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick] [--no-cpu]
+       python bench.py --only NAME [--calib-copy-mib N]   (profiling runs: one
+       config, then an optional device copy of N MiB used to calibrate counters)
 """
 from __future__ import annotations
 
@@ -17,6 +20,7 @@ import argparse
 import json
 import math
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -55,8 +59,36 @@ def make_x(M, K, seed, dev, outliers):
     return x.contiguous()
 
 
+def _graph(fn, n):
+    """Capture n calls fn(i) into one HIP graph on torch's capture stream."""
+    import torch
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n):
+            fn(i)
+    return g
+
+
+def _time_graph(g, reps=1):
+    import torch
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1)  # ms
+
+
 def time_linear(name, M, K, N, seed, dev, steps, warmup, outliers=True):
-    """Per step: device quantize of x [M,K] + mat_mul against rotating weights."""
+    """Per step: device quantize of x [M,K] + mat_mul against rotating weights.
+
+    Steps are captured in one HIP graph (launch overhead of the Python caller is not
+    part of the GPU's work) and replayed once: exactly `steps` timed steps.  A second
+    graph holds only the matmul launches, for the kernel's own average duration.
+    """
     import torch
     from jjjetson_ops_amd import capi
 
@@ -66,50 +98,35 @@ def time_linear(name, M, K, N, seed, dev, steps, warmup, outliers=True):
     x = make_x(M, K, seed + 1000, dev, outliers)
     xq = torch.empty(capi.q8_1_output_bytes([K, M]), dtype=torch.uint8, device=dev)
     y = torch.empty(M * N, dtype=torch.float32, device=dev)
-    s = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
 
-    def step(i, rec):
+    def step(i):
         capi.quantize_q8_1(x, xq, [K, M])
-        if rec:
-            ev[i][0].record(s)
         capi.mat_mul(ws[i % copies], xq, y, K, N, M)
-        if rec:
-            ev[i][1].record(s)
+
+    def mm_only(i):
+        capi.mat_mul(ws[i % copies], xq, y, K, N, M)
 
     for i in range(warmup):
-        step(i, False)
+        step(i)
     torch.cuda.synchronize()
-    # timed region 1: whole steps, no per-kernel events
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record(s)
-    for i in range(steps):
-        step(i, False)
-    t1.record(s)
-    torch.cuda.synchronize()
-    ms_step = t0.elapsed_time(t1) / steps
-    # timed region 2: per-launch events around the matmul kernel
-    for i in range(steps):
-        step(i, True)
-    torch.cuda.synchronize()
-    kern_ms = sorted(a.elapsed_time(b) for a, b in ev)
-    kern_avg = sum(kern_ms) / len(kern_ms)
-    kern_med = kern_ms[len(kern_ms) // 2]
-    del ws
+    g_step = _graph(step, steps)
+    g_mm = _graph(mm_only, steps)
+    g_step.replay()
+    g_mm.replay()
+    ms_step = _time_graph(g_step) / steps
+    kern_ms = _time_graph(g_mm) / steps
+    del g_step, g_mm, ws
     torch.cuda.empty_cache()
     alg_bytes = wbytes + M * (K // 128) * 144 + 4 * M * N
     ops = 2.0 * M * N * K
     return {
         "name": name, "M": M, "K": K, "N": N, "weight_bytes": wbytes, "weight_copies": copies,
-        "ms_per_step": ms_step, "us_per_step": ms_step * 1e3,
-        "kernel_us_avg": kern_avg * 1e3, "kernel_us_median": kern_med * 1e3,
+        "ms_per_step": ms_step, "us_per_step": ms_step * 1e3, "kernel_us_avg": kern_ms * 1e3,
         "step_weight_GBps": wbytes / (ms_step * 1e-3) / 1e9,
-        "kernel_GBps": alg_bytes / (kern_avg * 1e-3) / 1e9,
-        "kernel_hbm_frac": alg_bytes / (kern_avg * 1e-3) / 1e9 / HBM_PEAK_GBS,
-        "kernel_TOPS": ops / (kern_avg * 1e-3) / 1e12,
-        "kernel_mfma_frac": ops / (kern_avg * 1e-3) / 1e12 / INT8_PEAK_TOPS,
+        "kernel_GBps": alg_bytes / (kern_ms * 1e-3) / 1e9,
+        "kernel_hbm_frac": alg_bytes / (kern_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "kernel_TOPS": ops / (kern_ms * 1e-3) / 1e12,
+        "kernel_mfma_frac": ops / (kern_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS,
         "alg_bytes_per_launch": alg_bytes, "ops_per_launch": ops,
     }
 
@@ -131,7 +148,7 @@ def time_moe(dev, steps, warmup):
     R = T * topk
     wbytes = E * N * (K // 32) * 18
     copies = max(2, math.ceil(ROTATE_BYTES / wbytes))
-    w_one = torch.cat(make_weights(N, K, 40, dev, 1) + [make_weights(N, K, 41 + e, dev, 1)[0] for e in range(E - 1)])
+    w_one = torch.cat([make_weights(N, K, 40 + e, dev, 1)[0] for e in range(E)])
     ws = [w_one] + [w_one.clone() for _ in range(copies - 1)]
     x = make_x(T, K, 45, dev, True)
     xr = x[(order // topk).to(dev)].contiguous()            # routed rows sorted by expert
@@ -139,28 +156,37 @@ def time_moe(dev, steps, warmup):
     y = torch.empty(R * N, dtype=torch.float32, device=dev)
     off_d = offsets.to(dev)
     dst_d = order.to(torch.int32).to(dev)
-    s = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    for i in range(warmup + steps):
-        capi.quantize_q8_1(xr, xq, [K, R])
-        j = i - warmup
-        if j >= 0:
-            ev[j][0].record(s)
+    capi.quantize_q8_1(xr, xq, [K, R])
+
+    def mm(i):
         capi.grouped_mat_mul(ws[i % copies], xq, off_d, y, K, N, R, route_dst=dst_d)
-        if j >= 0:
-            ev[j][1].record(s)
-    torch.cuda.synchronize()
-    kern = sorted(a.elapsed_time(b) for a, b in ev)
-    avg = sum(kern) / len(kern)
+
+    for i in range(warmup):
+        mm(i)
+    gr = _graph(mm, steps)
+    gr.replay()
+    avg = _time_graph(gr) / steps
     ops = 2.0 * R * N * K
     alg_bytes = wbytes + R * (K // 128) * 144 + 4 * R * N
-    del ws, w_one
+    del gr, ws, w_one
     torch.cuda.empty_cache()
     return {"name": "moe_grouped_e8_top2_t512", "routes": R, "K": K, "N": N,
-            "expert_counts": counts.tolist(), "kernel_us_avg": avg * 1e3, "kernel_us_median": kern[len(kern) // 2] * 1e3,
+            "expert_counts": counts.tolist(), "kernel_us_avg": avg * 1e3,
             "kernel_TOPS": ops / (avg * 1e-3) / 1e12, "kernel_mfma_frac": ops / (avg * 1e-3) / 1e12 / INT8_PEAK_TOPS,
             "kernel_GBps": alg_bytes / (avg * 1e-3) / 1e9,
             "kernel_hbm_frac": alg_bytes / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
+def _traffic(workload):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary (FETCH_SIZE and
+    WRITE_SIZE, each scaled by the same counters' reading for a torch copy kernel of
+    known size).  None when no summary for the workload is committed."""
+    path = ROOT / "profiles" / f"{workload}_pmc.md"
+    try:
+        m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", path.read_text())
+        return int(m.group(1)) if m else None
+    except OSError:
+        return None
 
 
 def cpu_baseline(M, K, N, budget_s=10.0):
@@ -224,6 +250,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline config only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default=None, help="run one config and print its result (profiling)")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="with --only: finish with a device copy of this many MiB (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: the path's multi-GPU sharding is "
@@ -236,20 +265,44 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
+    plan = [
+        ("gemv_m1_k4096_n11008", 1, 4096, 11008, 1, args.steps),
+        ("gemv_m1_k11008_n4096", 1, 11008, 4096, 1, args.steps),
+        ("m4_k4096_n14336", 4, 4096, 14336, 2, args.steps),
+        ("m8_k4096_n14336", 8, 4096, 14336, 2, args.steps),
+        ("m16_k4096_n14336", 16, 4096, 14336, 2, args.steps),
+        ("prefill_m2048_k4096_n4096", 2048, 4096, 4096, 3, max(20, args.steps // 4)),
+        ("prefill_m2048_k4096_n14336", 2048, 4096, 14336, 3, max(20, args.steps // 4)),
+    ]
+    if args.only:
+        if args.only == "moe_grouped_e8_top2_t512":
+            res = time_moe(dev, max(10, args.steps // 10), 3)
+        else:
+            sel = [p for p in plan if p[0] == args.only]
+            if not sel:
+                sys.exit(f"unknown config {args.only}; choose from {[p[0] for p in plan]} or moe_grouped_e8_top2_t512")
+            name, M, K, N, seed, st = sel[0]
+            res = time_linear(name, M, K, N, seed, dev, st, args.warmup)
+        if args.calib_copy_mib:
+            # A plain device copy of known size, for scaling FETCH_SIZE / WRITE_SIZE.
+            # The source is pushed out of L2 and the 256 MB MALL first by writing 1 GiB.
+            n = args.calib_copy_mib << 20
+            src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+            dst = torch.empty_like(src)
+            evict = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(2)
+            torch.cuda.synchronize()
+            del evict
+            dst.copy_(src)
+            torch.cuda.synchronize()
+        print(json.dumps(res), flush=True)
+        return
+
     log("bench: headline GEMV M=1 K=4096 N=11008")
-    head = time_linear("gemv_m1_k4096_n11008", 1, 4096, 11008, 1, dev, args.steps, args.warmup)
+    name, M, K, N, seed, st = plan[0]
+    head = time_linear(name, M, K, N, seed, dev, st, args.warmup)
     configs = [head]
     if not args.quick:
-        small_steps = max(20, args.steps // 4)
-        plan = [
-            ("gemv_m1_k11008_n4096", 1, 11008, 4096, 1, args.steps),
-            ("m4_k4096_n14336", 4, 4096, 14336, 2, args.steps),
-            ("m8_k4096_n14336", 8, 4096, 14336, 2, args.steps),
-            ("m16_k4096_n14336", 16, 4096, 14336, 2, args.steps),
-            ("prefill_m2048_k4096_n4096", 2048, 4096, 4096, 3, small_steps),
-            ("prefill_m2048_k4096_n14336", 2048, 4096, 14336, 3, small_steps),
-        ]
-        for name, M, K, N, seed, st in plan:
+        for name, M, K, N, seed, st in plan[1:]:
             log(f"bench: {name}")
             configs.append(time_linear(name, M, K, N, seed, dev, st, max(3, args.warmup // 4)))
         log("bench: moe grouped")
@@ -261,9 +314,10 @@ def main():
         cpu = cpu_baseline(1, 4096, 11008)
 
     roof = {"bound": "hbm", "achieved": head["kernel_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": head["kernel_GBps"] / HBM_PEAK_GBS, "traffic": None,
-            "kernel": "gemv_q4_0_q8_1_kernel<1,4>", "alg_bytes_per_launch": head["alg_bytes_per_launch"],
-            "kernel_us_avg": head["kernel_us_avg"]}
+            "frac": head["kernel_GBps"] / HBM_PEAK_GBS, "traffic": _traffic("gemv_m1_k4096_n11008"),
+            "kernel": "gemv_q4_0_q8_1_kernel<1,4,1,4>", "alg_bytes_per_launch": head["alg_bytes_per_launch"],
+            "kernel_us_avg": head["kernel_us_avg"],
+            "timing": "HIP graph of back-to-back launches on the launch stream, torch.cuda.Event around the replay"}
     gemm = next((c for c in configs if c["name"] == "prefill_m2048_k4096_n14336"), None)
     line = {
         "metric": METRIC,

@@ -32,6 +32,9 @@ HIP_FLAGS = [
     # No packed-FP32 (v_pk_*_f32) code generation on this target.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
+    # Keep MFMA sources/results in arch VGPRs: the epilogues read every MFMA result
+    # with VALU ops, which cannot take AGPR operands (no v_accvgpr copies).
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{INCLUDE}",
     f"-I{CSRC}",
 ]

@@ -120,13 +120,14 @@ int validate_mm(const void *w, const void *xq, const void *y, int K, int N, int 
 }
 
 int run_mm(const void *w, const void *xq, float *y, int K, int N, int M, int algo, hipStream_t s) {
-    if (algo == JJO_ALGO_AUTO) algo = (M <= kGemvMaxBatch) ? JJO_ALGO_GEMV_DOT4 : JJO_ALGO_MFMA;
+    if (algo == JJO_ALGO_AUTO)
+        algo = (M <= kGemvMaxBatch && K <= kGemvMaxK) ? JJO_ALGO_GEMV_DOT4 : JJO_ALGO_MFMA;
     hipError_t e;
     if (algo == JJO_ALGO_GEMV_DOT4) {
         if (M > kGemvMaxBatch)
             return set_error(JJO_ERR_INVALID_ARG, "dot4 GEMV supports batch <= %d (got %d)", kGemvMaxBatch, M);
-        if ((int64_t)M * (K / kQSuper) * kQ8BlockBytes > 160 * 1024)
-            return set_error(JJO_ERR_INVALID_ARG, "dot4 GEMV: batch*K too large for LDS staging");
+        if (K > kGemvMaxK)
+            return set_error(JJO_ERR_INVALID_ARG, "dot4 GEMV supports ncols_k <= %d (got %d)", kGemvMaxK, K);
         e = launch_gemv_dot4(w, xq, y, K, N, M, s);
         if (e != hipSuccess) return hip_fail(e, "gemv_q4_0_q8_1 launch");
     } else if (algo == JJO_ALGO_MFMA) {

@@ -53,22 +53,26 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int BN = 128;          // weight rows per workgroup
 constexpr int BM = 128;          // tokens per workgroup
-constexpr int KB = 8;            // 32-blocks per stage (K = 256)
+constexpr int KB = 4;            // 32-blocks per stage (K = 128: one Q8_1 superblock)
 constexpr int kThreads = 256;
 
-// LDS carve-up (bytes)
-constexpr int kXsBytes = 2 * BM * kQ8BlockBytes;         // 36864: [2 superblocks][BM][144]
-constexpr int kWqStride = KB * 32 + 16;                  // 272: one row's 8 unpacked blocks + pad
-constexpr int kWqBytes = BN * kWqStride;                 // 34816
+// LDS carve-up (bytes).  56 KB per workgroup, so two workgroups share a CU.
+constexpr int kXsBytes = BM * kQ8BlockBytes;             // 18432 per stage: [BM][144]
+constexpr int kWqStride = KB * 32 + 16;                  // 144: one row's 4 unpacked blocks + pad
+constexpr int kWqBytes = BN * kWqStride;                 // 18432
 constexpr int kWdEpiBytes = KB * BN * 2;                 // [KB][BN] fp16, rows permuted
 constexpr int kWdRowBytes = BN * KB * 2;                 // [BN][KB] fp16
-constexpr int kOffWq = kXsBytes;
+constexpr int kOffWq = 2 * kXsBytes;                     // activations are double-buffered
 constexpr int kOffWdEpi = kOffWq + kWqBytes;
 constexpr int kOffWdRow = kOffWdEpi + kWdEpiBytes;
-constexpr int kSmemBytes = kOffWdRow + kWdRowBytes;      // 75776
+constexpr int kSmemBytes = kOffWdRow + kWdRowBytes;      // 57344
+constexpr int kXUnits = kXsBytes / 16;                   // 1152 16-byte units per stage
+constexpr int kXRuns = kXUnits / 64;                     // 18 wave-sized (1 KB) runs
 
 constexpr uint32_t kBiasBits = 0x4B400000u;              // 1.5 * 2^23
 constexpr float kBias = 12582912.0f;
+
+typedef __attribute__((address_space(3))) void lds_void;
 
 // Position of tile-local row r (0..31) in the epilogue scale layout: the 16 rows
 // a lane half owns in the 32x32 MFMA output (rows 8q + 4h + i) become contiguous.
@@ -77,18 +81,24 @@ __device__ __forceinline__ int epi_perm(int r) {
     return h * 16 + q * 4 + i;
 }
 
-struct Staged {
-    uint32_t w[18];   // this thread's 4 raw Q4_0 blocks (72 bytes)
-    u32x4 x[9];       // this thread's 9 x 16 bytes of activation blocks
-};
+// Epilogue of one 32x32 int MFMA tile: acc += d_w * round(sumi * d_x / 8).
+__device__ __forceinline__ void epilogue(f32x16 &acc, const i32x16 &d, const uint32_t (&wv)[8], float dx8,
+                                         float nb8) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const f16x2 pr = __builtin_bit_cast(f16x2, wv[v >> 1]);
+        const float dwv = (float)((v & 1) ? pr.y : pr.x);
+        const float t = fmaf(__int_as_float(d[v]), dx8, nb8);
+        acc[v] = fmaf(dwv, t, acc[v]);
+    }
+}
 
 template <bool kGrouped>
-__global__ __launch_bounds__(kThreads, 1) void gemm_q4_0_q8_1_mfma_kernel(
+__global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     const uint8_t *__restrict__ w_all, const uint8_t *__restrict__ xq, float *__restrict__ y, int K,
     int N, int M, const int32_t *__restrict__ expert_offsets, int n_experts,
     const int32_t *__restrict__ route_dst) {
     extern __shared__ __align__(16) uint8_t smem[];
-    uint8_t *xs = smem;
     uint8_t *wq = smem + kOffWq;
     _Float16 *wd_epi = reinterpret_cast<_Float16 *>(smem + kOffWdEpi);
     _Float16 *wd_row = reinterpret_cast<_Float16 *>(smem + kOffWdRow);
@@ -104,7 +114,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q4_0_q8_1_mfma_kernel(
     const int n0 = blockIdx.x * BN;
     const size_t row_bytes = (size_t)(K / kQK) * kQ4BlockBytes;
     const int nb = K / kQK;
-    const int n_chunks = (nb + KB - 1) / KB;
+    const int n_stages = nb / KB;  // K % 128 == 0
 
     // ---- token range of this workgroup ----
     int m0, m_end;
@@ -114,6 +124,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q4_0_q8_1_mfma_kernel(
         int t = blockIdx.y;
         int e = 0;
         m0 = -1;
+        m_end = 0;
         for (; e < n_experts; ++e) {
             const int beg = expert_offsets[e], end = expert_offsets[e + 1];
             const int tiles = (end - beg + BM - 1) / BM;
@@ -131,66 +142,63 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q4_0_q8_1_mfma_kernel(
         m_end = M;
     }
 
-    // ---- staging helpers ----
-    const int st_row = tid >> 1;    // W: one row, half of the 8 blocks per thread
+    // ---- staging: weights through registers, activations by LDS DMA ----
+    const int st_row = tid >> 1;    // W: one row, one block pair per thread
     const int st_half = tid & 1;
-    const int st_grow = min(n0 + st_row, N - 1);
+    const uint8_t *w_src = w + (size_t)min(n0 + st_row, N - 1) * row_bytes + (size_t)st_half * 36;
+    uint32_t wst[9];                // this thread's 2 raw Q4_0 blocks (36 bytes)
 
-    auto issue_loads = [&](Staged &s, int c) {
-        const int blk0 = c * KB + st_half * 4;
-        if (blk0 < nb) {
-            const uint8_t *p = w + (size_t)st_grow * row_bytes + (size_t)blk0 * kQ4BlockBytes;
+    auto load_w = [&](int c) {
+        const uint8_t *p = w_src + (size_t)c * (KB * kQ4BlockBytes);
+        const u32x4a4 a = *reinterpret_cast<const u32x4a4 *>(p);
+        const u32x4a4 b = *reinterpret_cast<const u32x4a4 *>(p + 16);
+        wst[0] = a.x; wst[1] = a.y; wst[2] = a.z; wst[3] = a.w;
+        wst[4] = b.x; wst[5] = b.y; wst[6] = b.z; wst[7] = b.w;
+        wst[8] = *reinterpret_cast<const uint32_t *>(p + 32);
+    };
+
+    // Activation tile of stage c = superblock c: tokens m0.. of one contiguous run.
+    // Wave `wave` moves 1 KB runs r = wave, wave+4, ... (< 18); lane l moves 16 bytes.
+    // Units past the last valid token re-read unit 0 (their LDS bytes are never used
+    // with a nonzero scale).
+    const size_t x_stride = (size_t)M * kQ8BlockBytes;  // bytes per superblock
+    const uint8_t *x_base = xq + (size_t)m0 * kQ8BlockBytes;
+    const int x_valid_units = min(BM, m_end - m0) * (kQ8BlockBytes / 16);
+    uint32_t x_off[5];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const u32x4a4 v = *reinterpret_cast<const u32x4a4 *>(p + 16 * i);
-                s.w[4 * i + 0] = v.x; s.w[4 * i + 1] = v.y; s.w[4 * i + 2] = v.z; s.w[4 * i + 3] = v.w;
-            }
-            const u32x2a4 v = *reinterpret_cast<const u32x2a4 *>(p + 64);
-            s.w[16] = v.x; s.w[17] = v.y;
-        } else {
+    for (int i = 0; i < 5; ++i) {
+        const int unit = (wave + 4 * i) * 64 + lane;
+        x_off[i] = unit < x_valid_units ? unit * 16 : 0;
+    }
+    auto load_x = [&](int c) {
+        uint8_t *xs = smem + (c & 1) * kXsBytes;
+        const uint8_t *src = x_base + (size_t)c * x_stride;
 #pragma unroll
-            for (int i = 0; i < 18; ++i) s.w[i] = 0u;
-        }
-#pragma unroll
-        for (int i = 0; i < 9; ++i) {
-            const int idx = tid + kThreads * i;        // 16-byte unit, 0..2303
-            const int sl = idx >= 1152 ? 1 : 0;
-            const int within = idx - sl * 1152;
-            const int tok = m0 + (within * 16) / kQ8BlockBytes;
-            const int sb = c * 2 + sl;
-            if (tok < m_end && sb * 4 < nb) {
-                const uint8_t *p = xq + ((size_t)sb * M + m0) * kQ8BlockBytes + (size_t)within * 16;
-                s.x[i] = *reinterpret_cast<const u32x4 *>(p);
-            } else {
-                s.x[i] = u32x4{0u, 0u, 0u, 0u};
-            }
+        for (int i = 0; i < 5; ++i) {
+            const int run = wave + 4 * i;
+            if (run < kXRuns)
+                __builtin_amdgcn_global_load_lds((const void *)(src + x_off[i]), (lds_void *)(xs + run * 1024), 16, 0, 0);
         }
     };
 
-    auto store_lds = [&](const Staged &s) {
+    auto store_w = [&]() {
 #pragma unroll
-        for (int i = 0; i < 9; ++i) {
-            const int idx = tid + kThreads * i;
-            *reinterpret_cast<u32x4 *>(xs + idx * 16) = s.x[i];
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            // block i of this thread's four: even blocks start dword-aligned, odd ones
-            // start 2 bytes into a dword (their nibbles are then dword-aligned).
+        for (int i = 0; i < 2; ++i) {
+            // Even block: scale in the low half of dword 0, nibbles from byte 2 on
+            // (re-aligned); odd block: scale in the high half of dword 4, nibbles in
+            // dwords 5..8.
             uint32_t q[4];
             uint32_t dbits;
-            const int base = 9 * (i >> 1);
-            if ((i & 1) == 0) {
-                dbits = s.w[base] & 0xffffu;
+            if (i == 0) {
+                dbits = wst[0] & 0xffffu;
 #pragma unroll
-                for (int k = 0; k < 4; ++k)
-                    q[k] = __builtin_amdgcn_alignbyte(s.w[base + k + 1], s.w[base + k], 2);
+                for (int k = 0; k < 4; ++k) q[k] = __builtin_amdgcn_alignbyte(wst[k + 1], wst[k], 2);
             } else {
-                dbits = s.w[base + 4] >> 16;
+                dbits = wst[4] >> 16;
 #pragma unroll
-                for (int k = 0; k < 4; ++k) q[k] = s.w[base + 5 + k];
+                for (int k = 0; k < 4; ++k) q[k] = wst[5 + k];
             }
-            const int b = st_half * 4 + i;
+            const int b = st_half * 2 + i;
             u32x4 lo, hi;
             lo.x = q[0] & 0x0f0f0f0fu; lo.y = q[1] & 0x0f0f0f0fu;
             lo.z = q[2] & 0x0f0f0f0fu; lo.w = q[3] & 0x0f0f0f0fu;
@@ -218,97 +226,94 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_q4_0_q8_1_mfma_kernel(
 #pragma unroll
     for (int v = 0; v < 16; ++v) bias[v] = (int32_t)kBiasBits;
 
-    Staged st;
-    issue_loads(st, 0);
+    // Columns past m_end hold stale LDS bytes: their scales are forced to zero.
+    const bool col_ok[2] = {m0 + wm * 64 + l32 < m_end, m0 + wm * 64 + 32 + l32 < m_end};
 
-    for (int c = 0; c < n_chunks; ++c) {
-        __syncthreads();          // previous stage's LDS reads are done
-        store_lds(st);
+    load_x(0);
+    load_w(0);
+
+    for (int c = 0; c < n_stages; ++c) {
+        // Stage c-1 compute is finished everywhere, so the W tile and activation
+        // buffer (c+1)&1 are free.  Waiting here also retires this thread's W(c) and
+        // X(c) loads, issued one full compute phase ago.
         __syncthreads();
-        if (c + 1 < n_chunks) issue_loads(st, c + 1);
+        store_w();
+        __syncthreads();          // W(c) unpacked and X(c) landed for every thread
+        // Loads of stage c+1 go out after the barrier, so nothing waits on them until
+        // the next iteration: their latency overlaps this stage's MFMA/epilogue work.
+        if (c + 1 < n_stages) {
+            load_x(c + 1);
+            load_w(c + 1);
+        }
 
-        const int kb_here = min(KB, nb - c * KB);  // multiple of 4
+        const uint8_t *xs = smem + (c & 1) * kXsBytes;
 
-        // Activation headers (d, s) of both superblocks for this lane's columns.
-        uint32_t hdr[2][2][4];  // [ct][sl][g]
+        // Activation headers (d, s) of this lane's two columns.
+        uint32_t hdr[2][4];
 #pragma unroll
         for (int ct = 0; ct < 2; ++ct) {
             const int col = wm * 64 + ct * 32 + l32;
-#pragma unroll
-            for (int sl = 0; sl < 2; ++sl) {
-                const u32x4 h = *reinterpret_cast<const u32x4 *>(xs + (sl * BM + col) * kQ8BlockBytes);
-                hdr[ct][sl][0] = h.x; hdr[ct][sl][1] = h.y; hdr[ct][sl][2] = h.z; hdr[ct][sl][3] = h.w;
-            }
+            const u32x4 h = *reinterpret_cast<const u32x4 *>(xs + col * kQ8BlockBytes);
+            hdr[ct][0] = col_ok[ct] ? h.x : 0u; hdr[ct][1] = col_ok[ct] ? h.y : 0u;
+            hdr[ct][2] = col_ok[ct] ? h.z : 0u; hdr[ct][3] = col_ok[ct] ? h.w : 0u;
         }
 
 #pragma unroll
         for (int b = 0; b < KB; ++b) {
-            if (b < kb_here) {
-                const int sl = b >> 2, g = b & 3;
-                i32x4 bop[2], aop[2];
+            i32x4 bop[2], aop[2];
 #pragma unroll
-                for (int ct = 0; ct < 2; ++ct) {
-                    const int col = wm * 64 + ct * 32 + l32;
-                    bop[ct] = *reinterpret_cast<const i32x4 *>(xs + (sl * BM + col) * kQ8BlockBytes +
-                                                               16 + 32 * g + 16 * hh);
-                }
-#pragma unroll
-                for (int rt = 0; rt < 2; ++rt) {
-                    const int row = wn * 64 + rt * 32 + l32;
-                    aop[rt] = *reinterpret_cast<const i32x4 *>(wq + row * kWqStride + b * 32 + 16 * hh);
-                }
-                i32x16 d[2][2];
-#pragma unroll
-                for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-                    for (int ct = 0; ct < 2; ++ct)
-                        d[rt][ct] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[rt], bop[ct], bias, 0, 0, 0);
-
-                float dx8[2], nb8[2];
-#pragma unroll
-                for (int ct = 0; ct < 2; ++ct) {
-                    const uint32_t ds = hdr[ct][sl][g];
-                    const float dx = __half2float(__ushort_as_half((unsigned short)(ds & 0xffffu)));
-                    dx8[ct] = dx * 0.125f;
-                    nb8[ct] = -kBias * dx8[ct];
-                }
-#pragma unroll
-                for (int rt = 0; rt < 2; ++rt) {
-                    const int rbase = (wn * 2 + rt) * 32 + hh * 16;
-                    const u32x4 w0 = *reinterpret_cast<const u32x4 *>(wd_epi + b * BN + rbase);
-                    const u32x4 w1 = *reinterpret_cast<const u32x4 *>(wd_epi + b * BN + rbase + 8);
-                    const uint32_t wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-                    for (int ct = 0; ct < 2; ++ct) {
-#pragma unroll
-                        for (int v = 0; v < 16; ++v) {
-                            const f16x2 pr = __builtin_bit_cast(f16x2, wv[v >> 1]);
-                            const float dwv = (float)((v & 1) ? pr.y : pr.x);
-                            const float t = fmaf(__int_as_float(d[rt][ct][v]), dx8[ct], nb8[ct]);
-                            acc[rt][ct][v] = fmaf(dwv, t, acc[rt][ct][v]);
-                        }
-                    }
-                }
+            for (int ct = 0; ct < 2; ++ct) {
+                const int col = wm * 64 + ct * 32 + l32;
+                bop[ct] = *reinterpret_cast<const i32x4 *>(xs + col * kQ8BlockBytes + 16 + 32 * b + 16 * hh);
             }
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                const int row = wn * 64 + rt * 32 + l32;
+                aop[rt] = *reinterpret_cast<const i32x4 *>(wq + row * kWqStride + b * 32 + 16 * hh);
+            }
+            float dx8[2], nb8[2];
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                const float dx = __half2float(__ushort_as_half((unsigned short)(hdr[ct][b] & 0xffffu)));
+                dx8[ct] = dx * 0.125f;
+                nb8[ct] = -kBias * dx8[ct];
+            }
+            uint32_t wv[2][8];
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                const int rbase = (wn * 2 + rt) * 32 + hh * 16;
+                const u32x4 w0 = *reinterpret_cast<const u32x4 *>(wd_epi + b * BN + rbase);
+                const u32x4 w1 = *reinterpret_cast<const u32x4 *>(wd_epi + b * BN + rbase + 8);
+                wv[rt][0] = w0.x; wv[rt][1] = w0.y; wv[rt][2] = w0.z; wv[rt][3] = w0.w;
+                wv[rt][4] = w1.x; wv[rt][5] = w1.y; wv[rt][6] = w1.z; wv[rt][7] = w1.w;
+            }
+            // Two result tiles in flight: the MFMA of the next tile overlaps the
+            // VALU epilogue of the previous one.
+            i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[0], bop[0], bias, 0, 0, 0);
+            i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[0], bop[1], bias, 0, 0, 0);
+            epilogue(acc[0][0], d0, wv[0], dx8[0], nb8[0]);
+            d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[1], bop[0], bias, 0, 0, 0);
+            epilogue(acc[0][1], d1, wv[0], dx8[1], nb8[1]);
+            d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[1], bop[1], bias, 0, 0, 0);
+            epilogue(acc[1][0], d0, wv[1], dx8[0], nb8[0]);
+            epilogue(acc[1][1], d1, wv[1], dx8[1], nb8[1]);
         }
 
-        // sum_b d_w * (-s_x) for the (up to) 8 blocks of this stage, on the f16 MFMA.
+        // sum_b d_w * (-s_x) over this stage's 4 blocks on the f16 MFMA (K = 8:
+        // the lanes of the upper K half contribute zeros).
         {
             f16x4 aop[2], bop[2];
 #pragma unroll
             for (int rt = 0; rt < 2; ++rt) {
                 const int row = wn * 64 + rt * 32 + l32;
-                aop[rt] = *reinterpret_cast<const f16x4 *>(wd_row + row * KB + 4 * hh);
+                aop[rt] = *reinterpret_cast<const f16x4 *>(wd_row + row * KB);
             }
-            const bool live = c * KB + 4 * hh < nb;
 #pragma unroll
             for (int ct = 0; ct < 2; ++ct) {
-                const uint32_t *h = hdr[ct][hh];
-                uint32_t lo = (h[0] >> 16) | (h[1] & 0xffff0000u);
-                uint32_t hi = (h[2] >> 16) | (h[3] & 0xffff0000u);
-                lo ^= 0x80008000u;
-                hi ^= 0x80008000u;
-                if (!live) { lo = 0u; hi = 0u; }
+                const uint32_t *h = hdr[ct];
+                uint32_t lo = ((h[0] >> 16) | (h[1] & 0xffff0000u)) ^ 0x80008000u;
+                uint32_t hi = ((h[2] >> 16) | (h[3] & 0xffff0000u)) ^ 0x80008000u;
+                if (hh) { lo = 0u; hi = 0u; }
                 const u32x2 pk = {lo, hi};
                 bop[ct] = __builtin_bit_cast(f16x4, pk);
             }

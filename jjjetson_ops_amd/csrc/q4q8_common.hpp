@@ -41,7 +41,9 @@ hipError_t launch_gemm_mfma_grouped(const void *w, const void *xq, const int32_t
 hipError_t launch_block_sums(const void *w, const void *xq, int32_t *sumi, int K, int N, int M,
                              hipStream_t stream);
 
-// Largest batch the dot4 GEMV kernel is instantiated for.
+// Largest batch / reduction length the dot4 GEMV kernel is instantiated for
+// (K is cut into at most 8 slices of 4096 values).
 constexpr int kGemvMaxBatch = 8;
+constexpr int kGemvMaxK = 8 * 4096;
 
 }  // namespace jjo
