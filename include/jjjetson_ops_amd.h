@@ -101,9 +101,21 @@ int mat_mul_q4_0_q8_1(const void *weight_q4_0, const float *input, uint8_t *quan
 int mat_mul_q4_0_q8_1_device(const void *d_w_q4_0, const void *d_x_q8_1, float *d_y, int ncols_k,
                              int nrows_out, int batch, void *stream);
 
+/*
+ * Device-pointer form of the reference's host mat_mul_q4_0_q8_1
+ * (src/cuda/mm_q4_0_q8_1.cu:318-380): quantizes the fp32 activation d_x
+ * ([ncols_k, batch], dim0 fastest, 16-byte aligned) into d_quant_workspace
+ * (batch*ncols_k/128*144 bytes, quantizer layout; may be NULL when batch == 1
+ * and the caller does not need the Q8_1 bytes) and writes
+ * d_y[batch][nrows_out].  At batch == 1 both happen in one fused kernel.  No
+ * allocation, asynchronous on `stream`.
+ */
+int mat_mul_q4_0_q8_1_f32_device(const void *d_w_q4_0, const float *d_x, void *d_quant_workspace,
+                                 float *d_y, int ncols_k, int nrows_out, int batch, void *stream);
+
 /* Kernel selector for mat_mul_q4_0_q8_1_device_algo. */
 #define JJO_ALGO_AUTO 0
-#define JJO_ALGO_GEMV_DOT4 1 /* streaming v_dot4 GEMV, batch <= 16 */
+#define JJO_ALGO_GEMV 1 /* streaming GEMV (v_dot8 on 4-bit planes), batch <= 8 */
 #define JJO_ALGO_MFMA 2      /* int8 MFMA tile GEMM, any batch */
 
 /*

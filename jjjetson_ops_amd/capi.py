@@ -19,7 +19,7 @@ JJO_ERR_HIP = 2
 JJO_ERR_NO_DEVICE = 3
 
 ALGO_AUTO = 0
-ALGO_GEMV_DOT4 = 1
+ALGO_GEMV = 1
 ALGO_MFMA = 2
 
 QK = 32
@@ -37,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "parse_q8_1_output",
     "mat_mul_q4_0_q8_1",
     "mat_mul_q4_0_q8_1_device",
+    "mat_mul_q4_0_q8_1_f32_device",
     "mat_mul_q4_0_q8_1_device_algo",
     "mat_mul_q4_0_q8_1_block_sums_device",
     "mat_mul_q4_0_q8_1_grouped_device",
@@ -79,6 +80,8 @@ def lib() -> ctypes.CDLL:
         L.mat_mul_q4_0_q8_1.argtypes = [vp, vp, vp, vp, i64p, i32, i32, i32]
         L.mat_mul_q4_0_q8_1_device.restype = i32
         L.mat_mul_q4_0_q8_1_device.argtypes = [vp, vp, vp, i32, i32, i32, vp]
+        L.mat_mul_q4_0_q8_1_f32_device.restype = i32
+        L.mat_mul_q4_0_q8_1_f32_device.argtypes = [vp, vp, vp, vp, i32, i32, i32, vp]
         L.mat_mul_q4_0_q8_1_device_algo.restype = i32
         L.mat_mul_q4_0_q8_1_device_algo.argtypes = [vp, vp, vp, i32, i32, i32, i32, vp]
         L.mat_mul_q4_0_q8_1_block_sums_device.restype = i32
@@ -154,6 +157,22 @@ def mat_mul(w, xq, y, K: int, N: int, M: int, algo: int = ALGO_AUTO, stream=None
         raise ValueError("output buffer too small")
     _check(lib().mat_mul_q4_0_q8_1_device_algo(_dev(w, "w"), _dev(xq, "xq"), _dev(y, "y"), K, N, M, algo,
                                                _stream(stream)), "mat_mul_q4_0_q8_1_device")
+
+
+def mat_mul_f32(w, x, xq, y, K: int, N: int, M: int, stream=None) -> None:
+    """Quantize fp32 x [M, K] (into xq, may be None when M == 1) and y[M, N] = W . x."""
+    import torch
+    if x.dtype != torch.float32 or y.dtype != torch.float32:
+        raise ValueError("x and y must be float32")
+    if x.numel() < M * K or y.numel() < M * N:
+        raise ValueError("x or y too small")
+    if xq is not None and xq.numel() * xq.element_size() < M * (K // QSUPER) * Q8_BLOCK_BYTES:
+        raise ValueError("Q8_1 workspace too small")
+    if w.numel() * w.element_size() < N * (K // QK) * Q4_BLOCK_BYTES:
+        raise ValueError("weight buffer too small")
+    xqp = _dev(xq, "xq") if xq is not None else ctypes.c_void_p(0)
+    _check(lib().mat_mul_q4_0_q8_1_f32_device(_dev(w, "w"), _dev(x, "x"), xqp, _dev(y, "y"), K, N, M,
+                                              _stream(stream)), "mat_mul_q4_0_q8_1_f32_device")
 
 
 def block_sums(w, xq, out, K: int, N: int, M: int, stream=None) -> None:

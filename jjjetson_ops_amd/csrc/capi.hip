@@ -121,13 +121,16 @@ int validate_mm(const void *w, const void *xq, const void *y, int K, int N, int 
 
 int run_mm(const void *w, const void *xq, float *y, int K, int N, int M, int algo, hipStream_t s) {
     if (algo == JJO_ALGO_AUTO)
-        algo = (M <= kGemvMaxBatch && K <= kGemvMaxK) ? JJO_ALGO_GEMV_DOT4 : JJO_ALGO_MFMA;
+        algo = (M <= kGemvMaxBatch && K <= kGemvMaxK && (int64_t)M * (K / 64) * 80 <= 150 * 1024)
+                   ? JJO_ALGO_GEMV : JJO_ALGO_MFMA;
     hipError_t e;
-    if (algo == JJO_ALGO_GEMV_DOT4) {
+    if (algo == JJO_ALGO_GEMV) {
         if (M > kGemvMaxBatch)
-            return set_error(JJO_ERR_INVALID_ARG, "dot4 GEMV supports batch <= %d (got %d)", kGemvMaxBatch, M);
+            return set_error(JJO_ERR_INVALID_ARG, "GEMV supports batch <= %d (got %d)", kGemvMaxBatch, M);
         if (K > kGemvMaxK)
-            return set_error(JJO_ERR_INVALID_ARG, "dot4 GEMV supports ncols_k <= %d (got %d)", kGemvMaxK, K);
+            return set_error(JJO_ERR_INVALID_ARG, "GEMV supports ncols_k <= %d (got %d)", kGemvMaxK, K);
+        if ((int64_t)M * (K / 64) * 80 > 150 * 1024)
+            return set_error(JJO_ERR_INVALID_ARG, "GEMV: batch*ncols_k too large for LDS staging (batch=%d K=%d)", M, K);
         e = launch_gemv_dot4(w, xq, y, K, N, M, s);
         if (e != hipSuccess) return hip_fail(e, "gemv_q4_0_q8_1 launch");
     } else if (algo == JJO_ALGO_MFMA) {
@@ -261,6 +264,27 @@ int mat_mul_q4_0_q8_1_device(const void *d_w_q4_0, const void *d_x_q8_1, float *
                                          JJO_ALGO_AUTO, stream);
 }
 
+int mat_mul_q4_0_q8_1_f32_device(const void *d_w_q4_0, const float *d_x, void *d_quant_workspace,
+                                 float *d_y, int ncols_k, int nrows_out, int batch, void *stream) {
+    clear_error();
+    const void *xq_check = d_quant_workspace != nullptr ? d_quant_workspace : (const void *)d_x;
+    int rc = validate_mm(d_w_q4_0, xq_check, d_y, ncols_k, nrows_out, batch);
+    if (rc != JJO_OK) return rc;
+    if (d_x == nullptr || !aligned(d_x, 16)) return set_error(JJO_ERR_INVALID_ARG, "activation pointer must be non-null and 16-byte aligned");
+    if ((rc = require_gfx950()) != JJO_OK) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    if (batch == 1 && ncols_k <= kGemvMaxK) {
+        hipError_t e = launch_gemv_fused(d_w_q4_0, d_x, d_quant_workspace, d_y, ncols_k, nrows_out, s);
+        if (e != hipSuccess) return hip_fail(e, "fused quantize+GEMV launch");
+        return JJO_OK;
+    }
+    if (d_quant_workspace == nullptr)
+        return set_error(JJO_ERR_INVALID_ARG, "quant workspace is required when batch > 1");
+    hipError_t e = launch_quantize_q8_1(d_x, d_quant_workspace, ncols_k, batch, 1, s);
+    if (e != hipSuccess) return hip_fail(e, "quantize_q8_1 launch");
+    return run_mm(d_w_q4_0, d_quant_workspace, d_y, ncols_k, nrows_out, batch, JJO_ALGO_AUTO, s);
+}
+
 int mat_mul_q4_0_q8_1_block_sums_device(const void *d_w_q4_0, const void *d_x_q8_1, int32_t *d_sumi,
                                         int ncols_k, int nrows_out, int batch, void *stream) {
     clear_error();
@@ -328,8 +352,7 @@ int mat_mul_q4_0_q8_1(const void *weight_q4_0, const float *input, uint8_t *quan
         if ((e = hipMalloc((void **)&dy, y_elems * sizeof(float))) != hipSuccess) { rc = hip_fail(e, "hipMalloc(y)"); break; }
         if ((e = hipMemcpyAsync(dx, input, n_in * sizeof(float), hipMemcpyHostToDevice, s)) != hipSuccess) { rc = hip_fail(e, "H2D x"); break; }
         if ((e = hipMemcpyAsync(dw, weight_q4_0, w_bytes, hipMemcpyHostToDevice, s)) != hipSuccess) { rc = hip_fail(e, "H2D w"); break; }
-        if ((e = launch_quantize_q8_1(dx, dq, d.K, T, 1, s)) != hipSuccess) { rc = hip_fail(e, "quantize_q8_1 launch"); break; }
-        if ((rc = run_mm(dw, dq, dy, ncols_k, nrows_out, (int)T, JJO_ALGO_AUTO, s)) != JJO_OK) break;
+        if ((rc = mat_mul_q4_0_q8_1_f32_device(dw, dx, dq, dy, ncols_k, nrows_out, (int)T, s)) != JJO_OK) break;
         if ((e = hipMemcpyAsync(quant_workspace, dq, q_bytes, hipMemcpyDeviceToHost, s)) != hipSuccess) { rc = hip_fail(e, "D2H xq"); break; }
         if ((e = hipMemcpyAsync(output, dy, y_elems * sizeof(float), hipMemcpyDeviceToHost, s)) != hipSuccess) { rc = hip_fail(e, "D2H y"); break; }
         if ((e = hipStreamSynchronize(s)) != hipSuccess) { rc = hip_fail(e, "hipStreamSynchronize"); break; }

@@ -9,20 +9,27 @@
 //   * The weight matrix is streamed exactly once.  A row is cut into K-slices of
 //     64 block pairs (4096 values, 2304 bytes); lane l of a wave owns the 36-byte
 //     pair l of the slice (two 18-byte blocks are 4-byte aligned together),
-//     fetched with dwordx4 + dwordx4 + dword, so one wave instruction triple
-//     covers a whole K=4096 row slice.
-//   * A wave owns U rows x one K-slice: it issues all its weight loads first,
-//     then reads its activation pair (M tokens x 72 bytes) straight from L2 into
-//     registers — every HBM request of the kernel is in flight at once, with no
-//     barrier in front of it.
-//   * Even block of a pair: scale in the low half of dword 0, nibbles at byte 2
-//     (re-aligned with v_alignbyte); odd block: scale in the high half of dword
-//     4, nibbles in dwords 5..8.  Nibbles are masked into int8 lanes for
-//     v_dot4_i32_i8: 16 dot4 per pair per token.
-//   * Lane partials are summed with DPP (quad perms, row rotates) and four
-//     v_readlane; the JS K-slices of a row group (JS waves of one workgroup)
-//     are then added through LDS in slice order.
+//     fetched with dwordx4 + dwordx4 + dword.  A wave owns U rows of one slice and
+//     issues all its weight loads before anything else.
+//   * Integer dot without unpacking nibbles: with u = q + 128 = 16*hi + lo
+//     (hi, lo in 0..15) the activation is split once into two 4-bit planes laid
+//     out in the weight's own nibble order (element j in the low nibble of byte
+//     j, element j+16 in the high nibble), so a raw Q4_0 nibble dword feeds
+//     v_dot8_u32_u4 directly:
+//        sumi = 16*dot8(w, HI) + dot8(w, LO) - 128*dot8(w, 0x11111111)
+//     (the last term depends on the weights only and is shared by all tokens).
+//   * While the weight loads are in flight, the workgroup builds those planes
+//     plus (d_x, -8*s_x) for every block of its K range in LDS: from the Q8_1
+//     blocks, or -- fused variant, M = 1 -- straight from the fp32 activation
+//     with the reference quantizer's arithmetic (exact sum tree, IEEE divides,
+//     roundf), optionally writing the Q8_1 bytes too.  One 80-byte LDS record
+//     per (token, block pair): conflict-free ds_read_b128 for consecutive lanes.
+//   * Lane partials: DPP quad/row rotations and four v_readlane; the JS
+//     K-slices of a row group (JS waves of one workgroup) are added in LDS in
+//     slice order.
 #include <hip/hip_fp16.h>
+
+#include <type_traits>
 
 #include "q4q8_common.hpp"
 
@@ -32,15 +39,12 @@ namespace {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x4a16 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2a8 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kRec = 80;  // LDS bytes per (token, block pair): HI a|LO a|HI b|LO b|dx a,c a,dx b,c b
 
 struct PairW {
     uint32_t d[9];
-};
-
-// Activation data of one block pair for one token: 16 int8x4 dwords + 2 (d,s) words.
-struct PairX {
-    uint32_t q[16];
-    uint32_t ds[2];
 };
 
 __device__ __forceinline__ void load_pair(PairW &w, const uint8_t *p) {
@@ -52,18 +56,6 @@ __device__ __forceinline__ void load_pair(PairW &w, const uint8_t *p) {
     w.d[8] = c;
 }
 
-// blk points at the 144-byte block of the pair's superblock; g0 = first group.
-__device__ __forceinline__ void load_x(PairX &x, const uint8_t *blk, int g0) {
-    const u32x2a8 ds = *reinterpret_cast<const u32x2a8 *>(blk + 4 * g0);
-    x.ds[0] = ds.x;
-    x.ds[1] = ds.y;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const u32x4a16 v = *reinterpret_cast<const u32x4a16 *>(blk + 16 + 32 * g0 + 16 * i);
-        x.q[4 * i + 0] = v.x; x.q[4 * i + 1] = v.y; x.q[4 * i + 2] = v.z; x.q[4 * i + 3] = v.w;
-    }
-}
-
 __device__ __forceinline__ float half_lo(uint32_t v) {
     return __half2float(__ushort_as_half((unsigned short)(v & 0xffffu)));
 }
@@ -71,17 +63,36 @@ __device__ __forceinline__ float half_hi(uint32_t v) {
     return __half2float(__ushort_as_half((unsigned short)(v >> 16)));
 }
 
-// Integer dot of one Q4_0 block's 4 nibble dwords with 8 activation dwords.
-__device__ __forceinline__ int32_t block_sumi(const uint32_t q[4], const uint32_t *x) {
-    int32_t s = 0;
+// Planes of one block from its 8 activation dwords (int8 q, element 4i+k in byte k
+// of dword i).  u = q ^ 0x80 per byte = q + 128.  Output dword i pairs element
+// 4i+k (low nibble of byte k) with element 16+4i+k (high nibble).
+__device__ __forceinline__ void make_planes(const uint32_t q[8], uint32_t hi[4], uint32_t lo[4]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int32_t lo = (int32_t)(q[i] & 0x0f0f0f0fu);
-        const int32_t hi = (int32_t)((q[i] >> 4) & 0x0f0f0f0fu);
-        s = __builtin_amdgcn_sdot4(lo, (int32_t)x[i], s, false);
-        s = __builtin_amdgcn_sdot4(hi, (int32_t)x[i + 4], s, false);
+        const uint32_t a = q[i] ^ 0x80808080u;
+        const uint32_t b = q[i + 4] ^ 0x80808080u;
+        lo[i] = (a & 0x0f0f0f0fu) | ((b & 0x0f0f0f0fu) << 4);
+        hi[i] = ((a >> 4) & 0x0f0f0f0fu) | (b & 0xf0f0f0f0u);
     }
-    return s;
+}
+
+// Integer sum of one Q4_0 block: w = its 4 raw nibble dwords, n128 = 128 * sum(nib).
+__device__ __forceinline__ int32_t block_sumi(const uint32_t w[4], const uint32_t hi[4], const uint32_t lo[4],
+                                              int32_t n128) {
+    uint32_t s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s = __builtin_amdgcn_udot8(w[i], hi[i], s, false);
+    s <<= 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s = __builtin_amdgcn_udot8(w[i], lo[i], s, false);
+    return (int32_t)s - n128;
+}
+
+__device__ __forceinline__ int32_t nib_sum128(const uint32_t w[4]) {
+    uint32_t n = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) n = __builtin_amdgcn_udot8(w[i], 0x11111111u, n, false);
+    return (int32_t)(n << 7);
 }
 
 template <int CTRL>
@@ -102,41 +113,213 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (r0 + r1) + (r2 + r3);
 }
 
+// Write one block's planes and constants into its half of the pair record.
+__device__ __forceinline__ void put_block(uint8_t *rec, int half, const uint32_t hi[4], const uint32_t lo[4],
+                                          float dx, float c) {
+    *reinterpret_cast<u32x4a16 *>(rec + 32 * half) = u32x4a16{hi[0], hi[1], hi[2], hi[3]};
+    *reinterpret_cast<u32x4a16 *>(rec + 32 * half + 16) = u32x4a16{lo[0], lo[1], lo[2], lo[3]};
+    reinterpret_cast<float *>(rec + 64)[2 * half] = dx;
+    reinterpret_cast<float *>(rec + 64)[2 * half + 1] = c;
+}
+
+// ---- activation staging from Q8_1 blocks (quantizer layout) ----
+// Item = (token m, block b).  Loads are issued first (issue_q8), the planes are
+// built once the data is there (finish_q8), so the weight requests can leave in
+// between.
+struct ItemQ8 {
+    uint32_t ds;
+    uint32_t q[8];
+};
+
+template <int M>
+__device__ __forceinline__ void issue_q8(ItemQ8 &it, const uint8_t *__restrict__ xq, int item, int nb) {
+    item = min(item, M * nb - 1);  // idle lanes re-read a valid item (no branch around the load)
+    const int m = item / nb, b = item - m * nb;
+    const uint8_t *blk = xq + ((size_t)(b >> 2) * M + m) * kQ8BlockBytes;
+    const int g = b & 3;
+    it.ds = *reinterpret_cast<const uint32_t *>(blk + 4 * g);
+    const u32x4a16 v0 = *reinterpret_cast<const u32x4a16 *>(blk + 16 + 32 * g);
+    const u32x4a16 v1 = *reinterpret_cast<const u32x4a16 *>(blk + 32 + 32 * g);
+    it.q[0] = v0.x; it.q[1] = v0.y; it.q[2] = v0.z; it.q[3] = v0.w;
+    it.q[4] = v1.x; it.q[5] = v1.y; it.q[6] = v1.z; it.q[7] = v1.w;
+}
+
+// Unconditional (no branch for the loads to sink into): items past the end write
+// the spare record `spare` after the M * nb/2 real ones.
+__device__ __forceinline__ void finish_q8(uint8_t *xs, const ItemQ8 &it, int item, int nb, int n_items) {
+    const int m = item / nb, b = item - m * nb;
+    uint32_t hi[4], lo[4];
+    make_planes(it.q, hi, lo);
+    const size_t rec = item < n_items ? (size_t)m * (nb >> 1) + (b >> 1) : (size_t)(n_items >> 1);
+    put_block(xs + rec * kRec, b & 1, hi, lo, half_lo(it.ds), -8.0f * half_hi(it.ds));
+}
+
+// ---- fused staging (M = 1): quantize fp32 x exactly as quantize_q8_1_kernel
+// (src/cuda/q8_1.cu:40-103).  Item = half of a 32-group; the two halves of a group
+// are adjacent lanes: h = 0 holds elements 0..7 and 16..23 (the reference's
+// virtual lanes t0, t1, t4, t5), h = 1 holds 8..15 and 24..31 (t2, t3, t6, t7).
+// The xor-4 partners are inside a lane, the xor-2 partners are exchanged with one
+// DPP quad_perm, and the group sum is ((t0+t4)+(t2+t6)) + ((t1+t5)+(t3+t7))
+// exactly as the reference's butterfly.
+struct ItemF32 {
+    f32x4 v[4];  // v[0], v[1]: elements 8h..8h+7; v[2], v[3]: 16+8h..16+8h+7
+};
+
+__device__ __forceinline__ void issue_f32(ItemF32 &it, const float *__restrict__ x, int item, int nb) {
+    const int b = min(item >> 1, nb - 1), h = item & 1;
+    const float *gx = x + (size_t)b * 32;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        it.v[i] = *reinterpret_cast<const f32x4 *>(gx + 8 * h + 4 * i);
+        it.v[2 + i] = *reinterpret_cast<const f32x4 *>(gx + 16 + 8 * h + 4 * i);
+    }
+}
+
+// roundf (ties away from zero) for |v| < 2^23 in three ops: adding 0.5 - 2^-25
+// with v's sign and truncating gives the same integer as roundf for every such
+// float (checked exhaustively over all 2^30 non-negative floats below 2^23 in
+// the test suite; the sign makes it symmetric).
+__device__ __forceinline__ int32_t round_away(float v) {
+    return __float2int_rz(v + copysignf(0.49999997f, v));
+}
+
+// All lanes of the wave must call this together (DPP partner exchange); `live`
+// masks the stores of items past the end.
+__device__ __forceinline__ void finish_f32(uint8_t *xs, uint8_t *__restrict__ xq_out, const ItemF32 &it, int item,
+                                           int nb, bool live) {
+    const int b = min(item >> 1, nb - 1), h = item & 1;
+    const f32x4 *v = it.v;
+    float am[4], su[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        am[i] = fmaxf(fabsf(v[i].x), fmaxf(fabsf(v[i].y), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+        float s = v[i].x + v[i].y;
+        s = s + v[i].z;
+        su[i] = s + v[i].w;
+    }
+    // xor-4 step (inside the lane): (t0+t4), (t1+t5) for h = 0; (t2+t6), (t3+t7) for h = 1
+    const float s0 = su[0] + su[2], s1 = su[1] + su[3];
+    const float m0 = fmaxf(am[0], am[2]), m1 = fmaxf(am[1], am[3]);
+    // xor-2 step: partner lane
+    const float s0o = dpp<0xB1>(s0), s1o = dpp<0xB1>(s1);
+    const float m0o = dpp<0xB1>(m0), m1o = dpp<0xB1>(m1);
+    // xor-1 step; additions are commutative, so both lanes get identical bits
+    const float sum = (s0 + s0o) + (s1 + s1o);
+    const float amax = fmaxf(fmaxf(m0, m0o), fmaxf(m1, m1o));
+    const float d_inv = (amax > 0.0f) ? 127.0f / amax : 0.0f;
+    uint32_t q[4];  // bytes of elements 8h..8h+7 (q[0], q[1]) and 16+8h.. (q[2], q[3])
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int32_t a = round_away(v[i].x * d_inv), bb = round_away(v[i].y * d_inv);
+        const int32_t c = round_away(v[i].z * d_inv), d = round_away(v[i].w * d_inv);
+        q[i] = (uint32_t)(a & 0xff) | ((uint32_t)(bb & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+               ((uint32_t)(d & 0xff) << 24);
+    }
+    if (!live) return;
+    // planes for weight dwords i = 2h, 2h+1 of block b
+    uint8_t *rec = xs + (size_t)(b >> 1) * kRec + 32 * (b & 1);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t a = q[i] ^ 0x80808080u;
+        const uint32_t bq = q[2 + i] ^ 0x80808080u;
+        reinterpret_cast<uint32_t *>(rec + 16)[2 * h + i] = (a & 0x0f0f0f0fu) | ((bq & 0x0f0f0f0fu) << 4);
+        reinterpret_cast<uint32_t *>(rec)[2 * h + i] = ((a >> 4) & 0x0f0f0f0fu) | (bq & 0xf0f0f0f0u);
+    }
+    const __half hd = __float2half_rn(1.0f / d_inv);
+    const __half hs = __float2half_rn(sum);
+    if (h == 0) {
+        float *cst = reinterpret_cast<float *>(xs + (size_t)(b >> 1) * kRec + 64) + 2 * (b & 1);
+        cst[0] = __half2float(hd);
+        cst[1] = -8.0f * __half2float(hs);
+    }
+    if (xq_out != nullptr) {
+        uint8_t *blk = xq_out + (size_t)(b >> 2) * kQ8BlockBytes;
+        const int g = b & 3;
+        *reinterpret_cast<u32x2a8 *>(blk + 16 + 32 * g + 8 * h) = u32x2a8{q[0], q[1]};
+        *reinterpret_cast<u32x2a8 *>(blk + 16 + 32 * g + 16 + 8 * h) = u32x2a8{q[2], q[3]};
+        if (h == 0)
+            *reinterpret_cast<uint32_t *>(blk + 4 * g) =
+                (uint32_t)__half_as_ushort(hd) | ((uint32_t)__half_as_ushort(hs) << 16);
+    }
+}
+
 // Workgroup = RG row groups x JS K-slices (one wave each).  JS = ceil(K / 4096).
-template <int M, int U, int JS, int RG>
+// FUSED: `xin` is the fp32 activation [K] (M = 1) instead of Q8_1 blocks and
+// `xq_out` (optional) receives its Q8_1 bytes (written by workgroup 0).
+template <int M, int U, int JS, int RG, bool FUSED, int EARLY>
 __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint8_t *__restrict__ w,
-                                                                      const uint8_t *__restrict__ xq,
-                                                                      float *__restrict__ y, int K,
-                                                                      int N) {
+                                                                      const void *__restrict__ xin,
+                                                                      uint8_t *__restrict__ xq_out,
+                                                                      float *__restrict__ y, int K, int N) {
+    extern __shared__ __align__(16) uint8_t xs[];  // M * K/64 records of kRec bytes + 1 spare
     __shared__ float part[JS > 1 ? RG * JS * U * M : 1];
 
+    constexpr int kThreadsWG = 64 * JS * RG;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int js = wave % JS;              // K-slice of this wave
     const int rg = wave / JS;              // row group inside the workgroup
-    const int P = K / 64;                  // block pairs per row
+    const int nb = K / kQK;
+    const int P = nb >> 1;                 // block pairs per row
     const int p = lane + 64 * js;          // this lane's pair
     const bool live = p < P;
-    const size_t row_bytes = (size_t)(K / kQK) * kQ4BlockBytes;
+    const size_t row_bytes = (size_t)nb * kQ4BlockBytes;
     const int r0 = (blockIdx.x * RG + rg) * U;
+    const int n_items = FUSED ? 2 * nb : M * nb;
+    const int rounds = (n_items + kThreadsWG - 1) / kThreadsWG;
 
-    // 1) weight requests for all U rows
-    PairW wb[U];
-    if (live) {
+    // All global loads below are unconditional (clamped addresses), so the
+    // compiler can count them and wait for exactly the ones each step needs.
+    // 1) activation requests (L2-resident): EARLY items per thread, ahead of the weights
+    using Item = typename std::conditional<FUSED, ItemF32, ItemQ8>::type;
+    Item early[EARLY];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int r = min(r0 + u, N - 1);
-            load_pair(wb[u], w + (size_t)r * row_bytes + (size_t)p * 36);
+    for (int r = 0; r < EARLY; ++r) {
+        const int item = threadIdx.x + r * kThreadsWG;
+        if constexpr (FUSED) {
+            issue_f32(early[r], reinterpret_cast<const float *>(xin), item, nb);
+        } else {
+            issue_q8<M>(early[r], reinterpret_cast<const uint8_t *>(xin), item, nb);
         }
     }
-    // 2) activation pair of every token (L2-resident, tiny)
-    PairX xr[M];
-    if (live) {
+    // Keep the instruction scheduler from hoisting the weight loads above them.
+    __builtin_amdgcn_sched_barrier(0);
+    // 2) weight requests for all U rows, in row order
+    PairW wb[U];
+    {
+        const int pl = min(p, P - 1);
 #pragma unroll
-        for (int m = 0; m < M; ++m)
-            load_x(xr[m], xq + ((size_t)(p >> 1) * M + m) * kQ8BlockBytes, (p & 1) * 2);
+        for (int u = 0; u < U; ++u) {
+            const int rr = min(r0 + u, N - 1);
+            load_pair(wb[u], w + (size_t)rr * row_bytes + (size_t)pl * 36);
+        }
     }
+    __builtin_amdgcn_sched_barrier(0);
+    // 3) activation planes of the whole K range in LDS, once per workgroup
+    uint8_t *xq_w = (FUSED && blockIdx.x == 0) ? xq_out : nullptr;
+#pragma unroll
+    for (int r = 0; r < EARLY; ++r) {
+        const int item = threadIdx.x + r * kThreadsWG;
+        if constexpr (FUSED) {
+            finish_f32(xs, xq_w, early[r], item, nb, item < n_items);
+        } else {
+            finish_q8(xs, early[r], item, nb, n_items);
+        }
+    }
+    for (int r = EARLY; r < rounds; ++r) {  // long activations: the rest, load-then-use
+        const int item = threadIdx.x + r * kThreadsWG;
+        Item it;
+        if constexpr (FUSED) {
+            issue_f32(it, reinterpret_cast<const float *>(xin), item, nb);
+            finish_f32(xs, xq_w, it, item, nb, item < n_items);
+        } else {
+            issue_q8<M>(it, reinterpret_cast<const uint8_t *>(xin), item, nb);
+            finish_q8(xs, it, item, nb, n_items);
+        }
+    }
+    __syncthreads();
 
+    // 4) rows in load order: the wait for row u covers only rows 0..u
     float acc[U][M];
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -152,14 +335,23 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
                 qa[i] = __builtin_amdgcn_alignbyte(wb[u].d[i + 1], wb[u].d[i], 2);
                 qb[i] = wb[u].d[i + 5];
             }
+            const int32_t na = nib_sum128(qa), nbs = nib_sum128(qb);
             const float dwa = half_lo(wb[u].d[0]);
             const float dwb = half_hi(wb[u].d[4]);
 #pragma unroll
             for (int m = 0; m < M; ++m) {
-                const int32_t sa = block_sumi(qa, xr[m].q);
-                const int32_t sb = block_sumi(qb, xr[m].q + 8);
-                float a = fmaf(dwa, fmaf((float)sa, half_lo(xr[m].ds[0]), -8.0f * half_hi(xr[m].ds[0])), 0.0f);
-                a = fmaf(dwb, fmaf((float)sb, half_lo(xr[m].ds[1]), -8.0f * half_hi(xr[m].ds[1])), a);
+                const uint8_t *rec = xs + ((size_t)m * P + p) * kRec;
+                const u32x4a16 ha = *reinterpret_cast<const u32x4a16 *>(rec);
+                const u32x4a16 la = *reinterpret_cast<const u32x4a16 *>(rec + 16);
+                const u32x4a16 hb = *reinterpret_cast<const u32x4a16 *>(rec + 32);
+                const u32x4a16 lb = *reinterpret_cast<const u32x4a16 *>(rec + 48);
+                const f32x4 cst = *reinterpret_cast<const f32x4 *>(rec + 64);
+                const uint32_t hia[4] = {ha.x, ha.y, ha.z, ha.w}, loa[4] = {la.x, la.y, la.z, la.w};
+                const uint32_t hib[4] = {hb.x, hb.y, hb.z, hb.w}, lob[4] = {lb.x, lb.y, lb.z, lb.w};
+                const int32_t sa = block_sumi(qa, hia, loa, na);
+                const int32_t sb = block_sumi(qb, hib, lob, nbs);
+                float a = dwa * fmaf((float)sa, cst.x, cst.y);
+                a = fmaf(dwb, fmaf((float)sb, cst.z, cst.w), a);
                 acc[u][m] = a;
             }
         }
@@ -199,51 +391,79 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
     }
 }
 
-template <int M, int U, int JS>
-hipError_t launch_js(const void *w, const void *xq, float *y, int K, int N, hipStream_t stream) {
-    constexpr int RG = JS >= 4 ? 1 : (JS == 3 ? 1 : 4 / JS);
+// Row groups per workgroup (the activation staging of a workgroup is shared by
+// its RG row groups of U rows).  Single-token decode favours wide workgroups of
+// short row groups; multi-token batches favour four row groups of four rows.
+template <int M, int JS>
+constexpr int rg_for() {
+    if (M == 1) return JS == 1 ? 8 : JS == 2 ? 4 : JS == 3 ? 4 : 2;
+    return JS == 1 ? 4 : JS == 2 ? 2 : 1;
+}
+
+template <int M, int U, int JS, bool FUSED, int EARLY>
+hipError_t launch_cfg(const void *w, const void *xin, uint8_t *xq_out, float *y, int K, int N, hipStream_t stream) {
+    constexpr int RG = rg_for<M, JS>();
     const int groups = (N + U - 1) / U;
     const int blocks = (groups + RG - 1) / RG;
-    hipLaunchKernelGGL((gemv_q4_0_q8_1_kernel<M, U, JS, RG>), dim3(blocks), dim3(64 * JS * RG), 0, stream,
-                       (const uint8_t *)w, (const uint8_t *)xq, y, K, N);
+    const size_t smem = ((size_t)M * (K / 64) + 1) * kRec;
+    if (smem > 64 * 1024) {
+        // Raise this instantiation's dynamic-LDS limit to what the call needs.
+        static size_t granted = 64 * 1024;
+        if (smem > granted) {
+            hipError_t e = hipFuncSetAttribute((const void *)gemv_q4_0_q8_1_kernel<M, U, JS, RG, FUSED, EARLY>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+            if (e != hipSuccess) return e;
+            granted = smem;
+        }
+    }
+    hipLaunchKernelGGL((gemv_q4_0_q8_1_kernel<M, U, JS, RG, FUSED, EARLY>), dim3(blocks), dim3(64 * JS * RG), smem,
+                       stream, (const uint8_t *)w, xin, xq_out, y, K, N);
     return hipGetLastError();
 }
 
-template <int M, int U>
-hipError_t launch_m(const void *w, const void *xq, float *y, int K, int N, hipStream_t stream) {
+template <int M, int U, int JS, bool FUSED>
+hipError_t launch_js(const void *w, const void *xin, uint8_t *xq_out, float *y, int K, int N, hipStream_t stream) {
+    constexpr int RG = rg_for<M, JS>();
+    const int n_items = FUSED ? 2 * (K / kQK) : M * (K / kQK);
+    const int rounds = (n_items + 64 * JS * RG - 1) / (64 * JS * RG);
+    if (rounds <= 1) return launch_cfg<M, U, JS, FUSED, 1>(w, xin, xq_out, y, K, N, stream);
+    if (rounds <= 2) return launch_cfg<M, U, JS, FUSED, 2>(w, xin, xq_out, y, K, N, stream);
+    return launch_cfg<M, U, JS, FUSED, 4>(w, xin, xq_out, y, K, N, stream);
+}
+
+template <int M, int U, bool FUSED>
+hipError_t launch_m(const void *w, const void *xin, uint8_t *xq_out, float *y, int K, int N, hipStream_t stream) {
     const int js = (K / 64 + 63) / 64;
     switch (js) {
-        case 1: return launch_js<M, U, 1>(w, xq, y, K, N, stream);
-        case 2: return launch_js<M, U, 2>(w, xq, y, K, N, stream);
-        case 3: return launch_js<M, U, 3>(w, xq, y, K, N, stream);
-        case 4: return launch_js<M, U, 4>(w, xq, y, K, N, stream);
-        case 5: return launch_js<M, U, 5>(w, xq, y, K, N, stream);
-        case 6: return launch_js<M, U, 6>(w, xq, y, K, N, stream);
-        case 7: return launch_js<M, U, 7>(w, xq, y, K, N, stream);
-        case 8: return launch_js<M, U, 8>(w, xq, y, K, N, stream);
-        default: return hipErrorInvalidValue;  // K > 32768: rejected by the C ABI
+        case 1: return launch_js<M, U, 1, FUSED>(w, xin, xq_out, y, K, N, stream);
+        case 2: return launch_js<M, U, 2, FUSED>(w, xin, xq_out, y, K, N, stream);
+        case 3: return launch_js<M, U, 3, FUSED>(w, xin, xq_out, y, K, N, stream);
+        case 4: return launch_js<M, U, 4, FUSED>(w, xin, xq_out, y, K, N, stream);
+        default: return hipErrorInvalidValue;  // K > 16384: the C ABI routes these to the MFMA GEMM
     }
 }
 
-#ifndef JJO_GEMV_U1
-#define JJO_GEMV_U1 4
-#endif
 
 }  // namespace
 
 hipError_t launch_gemv_dot4(const void *w, const void *xq, float *y, int K, int N, int M,
                             hipStream_t stream) {
     switch (M) {
-        case 1: return launch_m<1, JJO_GEMV_U1>(w, xq, y, K, N, stream);
-        case 2: return launch_m<2, 4>(w, xq, y, K, N, stream);
-        case 3: return launch_m<3, 4>(w, xq, y, K, N, stream);
-        case 4: return launch_m<4, 2>(w, xq, y, K, N, stream);
-        case 5: return launch_m<5, 2>(w, xq, y, K, N, stream);
-        case 6: return launch_m<6, 2>(w, xq, y, K, N, stream);
-        case 7: return launch_m<7, 1>(w, xq, y, K, N, stream);
-        case 8: return launch_m<8, 1>(w, xq, y, K, N, stream);
+        case 1: return launch_m<1, 2, false>(w, xq, nullptr, y, K, N, stream);
+        case 2: return launch_m<2, 4, false>(w, xq, nullptr, y, K, N, stream);
+        case 3: return launch_m<3, 4, false>(w, xq, nullptr, y, K, N, stream);
+        case 4: return launch_m<4, 4, false>(w, xq, nullptr, y, K, N, stream);
+        case 5: return launch_m<5, 2, false>(w, xq, nullptr, y, K, N, stream);
+        case 6: return launch_m<6, 2, false>(w, xq, nullptr, y, K, N, stream);
+        case 7: return launch_m<7, 2, false>(w, xq, nullptr, y, K, N, stream);
+        case 8: return launch_m<8, 2, false>(w, xq, nullptr, y, K, N, stream);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_gemv_fused(const void *w, const float *x, void *xq_out, float *y, int K, int N,
+                             hipStream_t stream) {
+    return launch_m<1, 2, true>(w, x, (uint8_t *)xq_out, y, K, N, stream);
 }
 
 }  // namespace jjo

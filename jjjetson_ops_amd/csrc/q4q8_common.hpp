@@ -33,6 +33,10 @@ hipError_t launch_quantize_q8_1(const float *x, void *y, int64_t K, int64_t ne1,
                                 hipStream_t stream);
 hipError_t launch_gemv_dot4(const void *w, const void *xq, float *y, int K, int N, int M,
                             hipStream_t stream);
+// M = 1 GEMV straight from the fp32 activation (quantized in-kernel, bit-exact with
+// launch_quantize_q8_1); xq_out (nullable) receives the Q8_1 bytes.
+hipError_t launch_gemv_fused(const void *w, const float *x, void *xq_out, float *y, int K, int N,
+                             hipStream_t stream);
 hipError_t launch_gemm_mfma(const void *w, const void *xq, float *y, int K, int N, int M,
                             hipStream_t stream);
 hipError_t launch_gemm_mfma_grouped(const void *w, const void *xq, const int32_t *expert_offsets,
@@ -42,8 +46,8 @@ hipError_t launch_block_sums(const void *w, const void *xq, int32_t *sumi, int K
                              hipStream_t stream);
 
 // Largest batch / reduction length the dot4 GEMV kernel is instantiated for
-// (K is cut into at most 8 slices of 4096 values).
+// (K is cut into at most 4 slices of 4096 values).
 constexpr int kGemvMaxBatch = 8;
-constexpr int kGemvMaxK = 8 * 4096;
+constexpr int kGemvMaxK = 4 * 4096;
 
 }  // namespace jjo

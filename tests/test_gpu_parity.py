@@ -115,7 +115,7 @@ def test_golden_small_case(dev):
     K, N, M = int(g["K"]), int(g["N"]), int(g["M"])
     note(f"golden mmq_small K={K} N={N} M={M}")
     assert np.array_equal(gpu_quantize(g["x"], [K, M], dev), g["xq"])
-    for algo in (capi.ALGO_GEMV_DOT4, capi.ALGO_MFMA):
+    for algo in (capi.ALGO_GEMV, capi.ALGO_MFMA):
         y = torch.full((M * N,), float("nan"), dtype=torch.float32, device=dev)
         capi.mat_mul(to_dev(g["w"], dev), to_dev(g["xq"], dev), y, K, N, M, algo=algo)
         torch.cuda.synchronize()
@@ -133,12 +133,12 @@ def run_mm(w, xq, K, N, M, algo, dev):
 
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
 @pytest.mark.parametrize("K,N", [(4096, 257), (11008, 64), (128, 5), (640, 96)])
-def test_gemv_dot4(K, N, M, dev):
-    note(f"gemv dot4 K={K} N={N} M={M}")
+def test_gemv(K, N, M, dev):
+    note(f"gemv K={K} N={N} M={M}")
     w = make_w(N, K, 7 * N + K)
     x = make_x(K, M, 100 + M)
     xq = c_oracle.quantize_q8_1(x, [K, M])
-    got = run_mm(w, xq, K, N, M, capi.ALGO_GEMV_DOT4, dev)
+    got = run_mm(w, xq, K, N, M, capi.ALGO_GEMV, dev)
     np.testing.assert_allclose(got, c_oracle.matmul(w, xq, K, N, M), rtol=RTOL, atol=ATOL)
 
 
@@ -154,6 +154,46 @@ def test_gemm_mfma(K, N, M, dev):
     np.testing.assert_allclose(got, c_oracle.matmul(w, xq, K, N, M), rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("K,N", [(4096, 11008), (11008, 4096), (128, 33), (640, 257), (4096, 5)])
+def test_fused_quantize_gemv(K, N, dev):
+    """mat_mul_q4_0_q8_1_f32_device at batch 1: the in-kernel quantization writes the
+    same Q8_1 bytes as the oracle (bit-exact) and y is within tolerance."""
+    import torch
+    note(f"fused quantize+GEMV K={K} N={N}")
+    w = make_w(N, K, K + 3 * N)
+    x = make_x(K, 1, K)
+    x[0, 64:96] = 2.5
+    x[0, 70] = 127.0           # d_inv = 1: ties round away from zero
+    xq_ref = c_oracle.quantize_q8_1(x, [K, 1])
+    xq = torch.zeros(xq_ref.size, dtype=torch.uint8, device=dev)
+    y = torch.full((N,), float("nan"), dtype=torch.float32, device=dev)
+    capi.mat_mul_f32(to_dev(w, dev), to_dev(x, dev), xq, y, K, N, 1)
+    torch.cuda.synchronize()
+    assert np.array_equal(xq.cpu().numpy(), xq_ref)
+    np.testing.assert_allclose(y.cpu().numpy().reshape(1, N), c_oracle.matmul(w, xq_ref, K, N, 1), rtol=RTOL, atol=ATOL)
+    # without a workspace
+    y2 = torch.full((N,), float("nan"), dtype=torch.float32, device=dev)
+    capi.mat_mul_f32(to_dev(w, dev), to_dev(x, dev), None, y2, K, N, 1)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("M", [2, 5])
+def test_f32_entry_batched(M, dev):
+    import torch
+    K, N = 512, 100
+    note(f"f32 entry batched M={M}")
+    w = make_w(N, K, 77)
+    x = make_x(K, M, 78)
+    xq_ref = c_oracle.quantize_q8_1(x, [K, M])
+    xq = torch.zeros(xq_ref.size, dtype=torch.uint8, device=dev)
+    y = torch.empty(M * N, dtype=torch.float32, device=dev)
+    capi.mat_mul_f32(to_dev(w, dev), to_dev(x, dev), xq, y, K, N, M)
+    torch.cuda.synchronize()
+    assert np.array_equal(xq.cpu().numpy(), xq_ref)
+    np.testing.assert_allclose(y.cpu().numpy().reshape(M, N), c_oracle.matmul(w, xq_ref, K, N, M), rtol=RTOL, atol=ATOL)
+
+
 def test_zero_activation_group_gives_nan_like_reference(dev):
     K, N, M = 256, 64, 2
     note("zero activation group -> NaN rows")
@@ -163,10 +203,16 @@ def test_zero_activation_group_gives_nan_like_reference(dev):
     xq = c_oracle.quantize_q8_1(x, [K, M])
     exp = c_oracle.matmul(w, xq, K, N, M)
     assert np.all(np.isnan(exp[1])) and np.all(np.isfinite(exp[0]))
-    for algo in (capi.ALGO_GEMV_DOT4, capi.ALGO_MFMA):
+    for algo in (capi.ALGO_GEMV, capi.ALGO_MFMA):
         got = run_mm(w, xq, K, N, M, algo, dev)
         assert np.all(np.isnan(got[1]))
         np.testing.assert_allclose(got[0], exp[0], rtol=RTOL, atol=ATOL)
+    # fused path, single token with a zero group
+    import torch
+    y = torch.empty(N, dtype=torch.float32, device=dev)
+    capi.mat_mul_f32(to_dev(w, dev), to_dev(x[1:2], dev), None, y, K, N, 1)
+    torch.cuda.synchronize()
+    assert np.all(np.isnan(y.cpu().numpy()))
 
 
 def test_mmq_host_entry_through_pybind(dev):
