@@ -21,6 +21,7 @@ JJO_ERR_NO_DEVICE = 3
 ALGO_AUTO = 0
 ALGO_GEMV = 1
 ALGO_MFMA = 2
+ALGO_SKINNY = 3
 
 QK = 32
 QSUPER = 128

@@ -120,9 +120,15 @@ int validate_mm(const void *w, const void *xq, const void *y, int K, int N, int 
 }
 
 int run_mm(const void *w, const void *xq, float *y, int K, int N, int M, int algo, hipStream_t s) {
-    if (algo == JJO_ALGO_AUTO)
-        algo = (M <= kGemvMaxBatch && K <= kGemvMaxK && (int64_t)M * (K / 64) * 80 <= 150 * 1024)
-                   ? JJO_ALGO_GEMV : JJO_ALGO_MFMA;
+    if (algo == JJO_ALGO_AUTO) {
+        const bool gemv_ok = M <= kGemvMaxBatch && K <= kGemvMaxK && (int64_t)M * (K / 64) * 80 <= 150 * 1024;
+        if (gemv_ok && M <= kGemvPreferredBatch)
+            algo = JJO_ALGO_GEMV;
+        else if (gemm_skinny_supported(w, xq, K, M))
+            algo = JJO_ALGO_SKINNY;
+        else
+            algo = gemv_ok ? JJO_ALGO_GEMV : JJO_ALGO_MFMA;
+    }
     hipError_t e;
     if (algo == JJO_ALGO_GEMV) {
         if (M > kGemvMaxBatch)
@@ -133,6 +139,13 @@ int run_mm(const void *w, const void *xq, float *y, int K, int N, int M, int alg
             return set_error(JJO_ERR_INVALID_ARG, "GEMV: batch*ncols_k too large for LDS staging (batch=%d K=%d)", M, K);
         e = launch_gemv_dot4(w, xq, y, K, N, M, s);
         if (e != hipSuccess) return hip_fail(e, "gemv_q4_0_q8_1 launch");
+    } else if (algo == JJO_ALGO_SKINNY) {
+        if (!gemm_skinny_supported(w, xq, K, M))
+            return set_error(JJO_ERR_INVALID_ARG,
+                             "skinny GEMM needs batch <= %d, ncols_k %% 256 == 0 and 16-byte aligned weights "
+                             "(batch=%d K=%d)", kSkinnyMaxBatch, M, K);
+        e = launch_gemm_skinny(w, xq, y, K, N, M, s);
+        if (e != hipSuccess) return hip_fail(e, "gemm_skinny launch");
     } else if (algo == JJO_ALGO_MFMA) {
         if ((M + 127) / 128 > 65535) return set_error(JJO_ERR_INVALID_ARG, "batch too large");
         e = launch_gemm_mfma(w, xq, y, K, N, M, s);

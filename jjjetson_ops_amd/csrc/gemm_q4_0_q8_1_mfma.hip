@@ -56,16 +56,18 @@ constexpr int BM = 128;          // tokens per workgroup
 constexpr int KB = 4;            // 32-blocks per stage (K = 128: one Q8_1 superblock)
 constexpr int kThreads = 256;
 
-// LDS carve-up (bytes).  56 KB per workgroup, so two workgroups share a CU.
+// LDS carve-up (bytes).  Activation and weight tiles are both double-buffered:
+// 76 KB per workgroup, so two workgroups share a CU.
 constexpr int kXsBytes = BM * kQ8BlockBytes;             // 18432 per stage: [BM][144]
 constexpr int kWqStride = KB * 32 + 16;                  // 144: one row's 4 unpacked blocks + pad
 constexpr int kWqBytes = BN * kWqStride;                 // 18432
 constexpr int kWdEpiBytes = KB * BN * 2;                 // [KB][BN] fp16, rows permuted
 constexpr int kWdRowBytes = BN * KB * 2;                 // [BN][KB] fp16
-constexpr int kOffWq = 2 * kXsBytes;                     // activations are double-buffered
-constexpr int kOffWdEpi = kOffWq + kWqBytes;
-constexpr int kOffWdRow = kOffWdEpi + kWdEpiBytes;
-constexpr int kSmemBytes = kOffWdRow + kWdRowBytes;      // 57344
+constexpr int kWBufBytes = kWqBytes + kWdEpiBytes + kWdRowBytes;  // one weight stage
+constexpr int kOffW = 2 * kXsBytes;
+constexpr int kOffWdEpi = kWqBytes;                      // offsets inside a weight stage
+constexpr int kOffWdRow = kWqBytes + kWdEpiBytes;
+constexpr int kSmemBytes = kOffW + 2 * kWBufBytes;       // 77824
 constexpr int kXUnits = kXsBytes / 16;                   // 1152 16-byte units per stage
 constexpr int kXRuns = kXUnits / 64;                     // 18 wave-sized (1 KB) runs
 
@@ -99,9 +101,6 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     int N, int M, const int32_t *__restrict__ expert_offsets, int n_experts,
     const int32_t *__restrict__ route_dst) {
     extern __shared__ __align__(16) uint8_t smem[];
-    uint8_t *wq = smem + kOffWq;
-    _Float16 *wd_epi = reinterpret_cast<_Float16 *>(smem + kOffWdEpi);
-    _Float16 *wd_row = reinterpret_cast<_Float16 *>(smem + kOffWdRow);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -181,7 +180,10 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
         }
     };
 
-    auto store_w = [&]() {
+    auto store_w = [&](int buf) {
+        uint8_t *wq = smem + kOffW + buf * kWBufBytes;
+        _Float16 *wd_epi = reinterpret_cast<_Float16 *>(wq + kOffWdEpi);
+        _Float16 *wd_row = reinterpret_cast<_Float16 *>(wq + kOffWdRow);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             // Even block: scale in the low half of dword 0, nibbles from byte 2 on
@@ -229,23 +231,23 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     // Columns past m_end hold stale LDS bytes: their scales are forced to zero.
     const bool col_ok[2] = {m0 + wm * 64 + l32 < m_end, m0 + wm * 64 + 32 + l32 < m_end};
 
+    // Pipeline, one barrier per stage: while stage c is computed from buffers c&1,
+    // the loads of stage c+1 are in flight; stage c+1's weights are unpacked into the
+    // other buffer right after, then one barrier publishes X(c+1) and W(c+1) and
+    // retires every wave's reads of buffers c&1, which stage c+2's loads then reuse.
     load_x(0);
     load_w(0);
+    store_w(0);               // waits for W(0) and, issued before it, X(0)
+    __syncthreads();
+    if (n_stages > 1) {
+        load_x(1);
+        load_w(1);
+    }
 
     for (int c = 0; c < n_stages; ++c) {
-        // Stage c-1 compute is finished everywhere, so the W tile and activation
-        // buffer (c+1)&1 are free.  Waiting here also retires this thread's W(c) and
-        // X(c) loads, issued one full compute phase ago.
-        __syncthreads();
-        store_w();
-        __syncthreads();          // W(c) unpacked and X(c) landed for every thread
-        // Loads of stage c+1 go out after the barrier, so nothing waits on them until
-        // the next iteration: their latency overlaps this stage's MFMA/epilogue work.
-        if (c + 1 < n_stages) {
-            load_x(c + 1);
-            load_w(c + 1);
-        }
-
+        uint8_t *wq = smem + kOffW + (c & 1) * kWBufBytes;
+        const _Float16 *wd_epi = reinterpret_cast<const _Float16 *>(wq + kOffWdEpi);
+        const _Float16 *wd_row = reinterpret_cast<const _Float16 *>(wq + kOffWdRow);
         const uint8_t *xs = smem + (c & 1) * kXsBytes;
 
         // Activation headers (d, s) of this lane's two columns.
@@ -322,6 +324,15 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
 #pragma unroll
                 for (int ct = 0; ct < 2; ++ct)
                     acc[rt][ct] = __builtin_amdgcn_mfma_f32_32x32x8f16(aop[rt], bop[ct], acc[rt][ct], 0, 0, 0);
+        }
+
+        if (c + 1 < n_stages) {
+            store_w((c + 1) & 1);  // waits for W(c+1) and X(c+1), issued a compute phase ago
+            __syncthreads();
+            if (c + 2 < n_stages) {
+                load_x(c + 2);
+                load_w(c + 2);
+            }
         }
     }
 

@@ -1,0 +1,306 @@
+// Small-batch (M <= 32) Q4_0 x Q8_1 matmul on gfx950 int8 matrix cores.
+//
+// Math is the reference's per-block epilogue (src/cuda/mm_q4_0_q8_1.cu:71-93):
+//     y[m][n] = sum_b d_w[n,b] * (sumi[n,m,b] * d_x[m,b] - 8 * s_x[m,b])
+//
+// At batch 2..32 the weight stream (0.5625 B per weight) still bounds the work, but
+// the per-token dot products no longer fit the VALU of a dot-product GEMV.  Here the
+// integer sums run on v_mfma_i32_16x16x32_i8 with the tokens as the MFMA rows and 16
+// weight rows as its columns, so one MFMA = 16 tokens x 16 weight rows x one 32-wide
+// K block, and an output lane holds four tokens of ONE weight row (one d_w per lane).
+//
+//   * Workgroup = 4 waves = 4 K-slices of the same RT*16 weight rows.  Each wave
+//     streams its slice through its own LDS ring of P stages; a stage is 8 K blocks:
+//       weights:     RT*16 rows x 144 B (8 Q4_0 blocks), row-major, 144 B per row
+//       activation:  the 2 Q8_1 superblocks of the stage for all M tokens, copied as
+//                    the one contiguous 288*M-byte run they occupy in the
+//                    quantizer's superblock-major layout
+//     Both move with global_load_lds_dwordx4 (global -> LDS, no VGPRs), so a stage is
+//     ~10 wide load instructions.  The wave waits for a stage with an explicit
+//     s_waitcnt vmcnt(n) (n = loads issued for the stages still in flight); there is
+//     no barrier inside the K loop.  The K-slice partials are added through LDS in
+//     slice order at the end.
+//   * K positions inside a block are permuted consistently for both operands: MFMA
+//     k-group g (lanes 16g..16g+15) takes elements 8g..8g+7, i.e. 8 contiguous
+//     activation bytes, and the weight nibbles of bytes 8(g&1)..8(g&1)+7, low
+//     nibbles for g < 2 and high nibbles for g >= 2.
+//   * The MFMA accumulator starts at 0x4B400000 (the bits of 1.5*2^23), so the
+//     result read as fp32 is 1.5*2^23 + sumi exactly and the epilogue needs no
+//     convert:
+//         t = fma(D, d_x/8, -1.5*2^23 * d_x/8)     (= round(sumi*d_x)/8)
+//         acc += d_w * (t - s_x)                    (= d_w*(sumi*d_x - 8*s_x)/8)
+//     The (d_x/8, -1.5*2^23*d_x/8, s_x) triples of a stage are converted once per
+//     stage into a wave-private LDS table.
+//
+// Requirements (checked by the launcher): K % 256 == 0, w and xq 16-byte aligned.
+#include <hip/hip_fp16.h>
+
+#include "q4q8_common.hpp"
+
+namespace jjo {
+namespace {
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kWaves = 4;  // K-slices per workgroup
+constexpr int kStageBlocks = 8;
+constexpr int kStageRowBytes = kStageBlocks * kQ4BlockBytes;  // 144
+constexpr uint32_t kBiasBits = 0x4B400000u;
+constexpr float kBias = 12582912.0f;
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] + [15:14],
+// expcnt[6:4] = 7, lgkmcnt[11:8] = 15).
+#define JJO_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n)&15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+#define JJO_LGKM0() __builtin_amdgcn_s_waitcnt(0xC07F)  // lgkmcnt(0); vmcnt 63 and expcnt 7 (no wait)
+// runtime wave-uniform count -> immediate
+__device__ __forceinline__ void vm_wait(int n) {
+    switch (n) {
+#define C_(k) \
+    case k: JJO_VMCNT(k); break;
+        C_(0) C_(1) C_(2) C_(3) C_(4) C_(5) C_(6) C_(7) C_(8) C_(9) C_(10) C_(11) C_(12) C_(13) C_(14) C_(15)
+        C_(16) C_(17) C_(18) C_(19) C_(20) C_(21) C_(22) C_(23) C_(24) C_(25) C_(26) C_(27) C_(28) C_(29)
+        C_(30) C_(31)
+#undef C_
+        default: JJO_VMCNT(0); break;
+    }
+}
+
+template <int RT, int CT>
+struct Geo {
+    static constexpr int kWChunks = RT * 16 * (kStageRowBytes / 16);  // 16-B chunks per stage
+    static constexpr int kWInstr = (kWChunks + 63) / 64;
+    static constexpr int kWBytes = kWChunks * 16;                    // RT * 2304
+    static constexpr int kXBytes = 2 * kQ8BlockBytes * 16 * CT;      // 288 * 16 * CT (max M)
+    static constexpr int kXInstrMax = (kXBytes / 16 + 63) / 64;
+    static constexpr int kStageBytes = kWBytes + kXBytes;
+    static constexpr int kScBytes = kStageBlocks * 3 * 16 * CT * 4;   // dx8, nb8, sx per block/token
+};
+
+template <int RT, int CT, int P>
+struct Lds {
+    static constexpr int kWaveBytes = P * Geo<RT, CT>::kStageBytes + Geo<RT, CT>::kScBytes;
+    static constexpr int kBytes = kWaves * kWaveBytes;
+    static constexpr int kRedBytes = kWaves * RT * CT * 64 * 16;
+    static_assert(kRedBytes <= kBytes, "reduction area must fit the rings");
+};
+
+template <int RT, int CT, int P>
+__global__ __launch_bounds__(64 * kWaves) void gemm_skinny_kernel(const uint8_t *__restrict__ w,
+                                                                  const uint8_t *__restrict__ xq,
+                                                                  float *__restrict__ y, int K, int N, int M) {
+    using G = Geo<RT, CT>;
+    using L = Lds<RT, CT, P>;
+    __shared__ __align__(16) uint8_t smem[L::kBytes];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15;
+    const int g = lane >> 4;
+    const int nb = K / kQK;
+    const int n_stages = nb / kStageBlocks;
+    const size_t row_bytes = (size_t)nb * kQ4BlockBytes;
+    const int n0 = blockIdx.x * (16 * RT);
+
+    // K-slice of this wave, in stages
+    const int per = (n_stages + kWaves - 1) / kWaves;
+    const int s_beg = min(n_stages, wave * per);
+    const int n_my = min(n_stages, s_beg + per) - s_beg;
+
+    uint8_t *ring = smem + wave * L::kWaveBytes;
+    float *sc = reinterpret_cast<float *>(ring + P * G::kStageBytes);
+
+    // ---- per-lane DMA sources ----
+    // weights: chunk c = 64*i + lane -> row c/9, 16-B piece c%9 of the row's stage bytes
+    uint32_t w_off[G::kWInstr];
+#pragma unroll
+    for (int i = 0; i < G::kWInstr; ++i) {
+        const int c = min(64 * i + lane, G::kWChunks - 1);
+        const int r = c / 9, piece = c % 9;
+        const int row = min(n0 + r, N - 1);
+        w_off[i] = (uint32_t)((size_t)(row - n0) * row_bytes) + 16u * piece;
+    }
+    const uint8_t *w_base = w + (size_t)n0 * row_bytes;
+    // activation: the stage's 288*M contiguous bytes
+    const int x_run = 2 * kQ8BlockBytes * M;
+    const int x_chunks = x_run / 16;
+    const int x_instr = (x_chunks + 63) / 64;  // wave-uniform, <= kXInstrMax
+    const int per_stage = G::kWInstr + x_instr;
+
+    auto issue = [&](int s) {  // stage s of this wave's slice into slot s % P
+        uint8_t *st = ring + (s % P) * G::kStageBytes;
+        const int gs = s_beg + s;
+        const uint8_t *ws = w_base + (size_t)gs * kStageRowBytes;
+#pragma unroll
+        for (int i = 0; i < G::kWInstr; ++i) {
+            if (64 * i + lane < G::kWChunks || (G::kWChunks % 64) == 0)
+                __builtin_amdgcn_global_load_lds((const void *)(ws + w_off[i]), (lds_void *)(st + 1024 * i), 16, 0, 0);
+        }
+        const uint8_t *xs = xq + (size_t)gs * x_run;
+        uint8_t *xd = st + G::kWBytes;
+#pragma unroll
+        for (int i = 0; i < G::kXInstrMax; ++i) {
+            if (i < x_instr) {  // wave-uniform
+                const int c = 64 * i + lane;
+                if (c < x_chunks)
+                    __builtin_amdgcn_global_load_lds((const void *)(xs + 16 * c), (lds_void *)(xd + 1024 * i), 16, 0,
+                                                     0);
+            }
+        }
+    };
+
+    i32x4 bias;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bias[i] = (int32_t)kBiasBits;
+    f32x4 acc[RT][CT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // token rows this lane feeds to the MFMA (clamped: rows >= M are never stored)
+    int a_tok_off[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) a_tok_off[ct] = min(16 * ct + l16, M - 1) * kQ8BlockBytes + 16 + 8 * g;
+    const int w_lane_off = l16 * kStageRowBytes + 2 + 8 * (g & 1);
+    const int w_shift = 4 * (g >> 1);
+
+    auto consume = [&](int s) {
+        const uint8_t *st = ring + (s % P) * G::kStageBytes;
+        const uint8_t *xs = st + G::kWBytes;
+        // activation scales of the stage -> sc[b][{dx8,nb8,sx}][token]
+        if (lane < 32 * CT) {
+            const int m = lane & (16 * CT - 1), h = lane / (16 * CT);
+            const uint32_t *ds = reinterpret_cast<const uint32_t *>(xs + h * kQ8BlockBytes * M +
+                                                                    min(m, M - 1) * kQ8BlockBytes);
+            const uint4 v = *reinterpret_cast<const uint4 *>(ds);
+            const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float dx8 = __half2float(__ushort_as_half((unsigned short)(vv[j] & 0xffffu))) * 0.125f;
+                const float sx = __half2float(__ushort_as_half((unsigned short)(vv[j] >> 16)));
+                float *row = sc + (4 * h + j) * 3 * 16 * CT;
+                row[m] = dx8;
+                row[16 * CT + m] = -kBias * dx8;
+                row[32 * CT + m] = sx;
+            }
+        }
+#pragma unroll
+        for (int bb = 0; bb < kStageBlocks; ++bb) {
+            const int h = bb >> 2, j = bb & 3;
+            long aop[CT];
+            f32x4 dx8[CT], nb8[CT], sx[CT];
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+                aop[ct] = *reinterpret_cast<const long *>(xs + h * kQ8BlockBytes * M + a_tok_off[ct] + 32 * j);
+                const float *row = sc + bb * 3 * 16 * CT + 16 * ct + 4 * g;
+                dx8[ct] = *reinterpret_cast<const f32x4 *>(row);
+                nb8[ct] = *reinterpret_cast<const f32x4 *>(row + 16 * CT);
+                sx[ct] = *reinterpret_cast<const f32x4 *>(row + 32 * CT);
+            }
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const uint8_t *wr = st + rt * 16 * kStageRowBytes + bb * kQ4BlockBytes;
+                uint32_t q0, q1;
+                if ((bb & 1) == 0) {  // nibbles at 2 mod 4: re-align three dwords
+                    const uint32_t *p = reinterpret_cast<const uint32_t *>(wr + w_lane_off - 2);
+                    const uint32_t d0 = p[0], d1 = p[1], d2 = p[2];
+                    q0 = __builtin_amdgcn_alignbyte(d1, d0, 2);
+                    q1 = __builtin_amdgcn_alignbyte(d2, d1, 2);
+                } else {
+                    const uint32_t *p = reinterpret_cast<const uint32_t *>(wr + w_lane_off);
+                    q0 = p[0];
+                    q1 = p[1];
+                }
+                const float dw = __half2float(
+                    __ushort_as_half(*reinterpret_cast<const unsigned short *>(wr + l16 * kStageRowBytes)));
+                const long bop =
+                    (long)(((uint64_t)((q1 >> w_shift) & 0x0f0f0f0fu) << 32) | ((q0 >> w_shift) & 0x0f0f0f0fu));
+#pragma unroll
+                for (int ct = 0; ct < CT; ++ct) {
+                    const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop[ct], bop, bias, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float t = fmaf(__int_as_float(d[i]), dx8[ct][i], nb8[ct][i]);
+                        acc[rt][ct][i] = fmaf(dw, t - sx[ct][i], acc[rt][ct][i]);
+                    }
+                }
+            }
+        }
+    };
+
+    if (n_my > 0) {
+        const int pre = min(P, n_my);
+        for (int s = 0; s < pre; ++s) issue(s);
+        for (int s = 0; s < n_my; ++s) {
+            const int ahead = min(P, n_my - s) - 1;  // stages issued after s
+            vm_wait(ahead * per_stage);
+            __builtin_amdgcn_sched_barrier(0);
+            consume(s);
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + P < n_my) {
+                JJO_LGKM0();  // slot s % P fully read before it is refilled
+                __builtin_amdgcn_sched_barrier(0);
+                issue(s + P);
+            }
+        }
+    }
+
+    // K-slice partials -> LDS (over the rings), summed in slice order by wave 0.
+    __syncthreads();
+    f32x4 *red = reinterpret_cast<f32x4 *>(smem);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) red[((wave * RT + rt) * CT + ct) * 64 + lane] = acc[rt][ct];
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct) {
+                f32x4 sum = red[((0 * RT + rt) * CT + ct) * 64 + lane];
+#pragma unroll
+                for (int k = 1; k < kWaves; ++k) sum = sum + red[((k * RT + rt) * CT + ct) * 64 + lane];
+                const int n = n0 + 16 * rt + l16;
+                if (n < N) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int m = 16 * ct + 4 * g + i;
+                        if (m < M) y[(size_t)m * N + n] = 8.0f * sum[i];
+                    }
+                }
+            }
+    }
+}
+
+template <int RT, int CT, int P>
+hipError_t launch_rcp(const void *w, const void *xq, float *y, int K, int N, int M, hipStream_t stream) {
+    const int blocks = (N + 16 * RT - 1) / (16 * RT);
+    hipLaunchKernelGGL((gemm_skinny_kernel<RT, CT, P>), dim3(blocks), dim3(64 * kWaves), 0, stream,
+                       (const uint8_t *)w, (const uint8_t *)xq, y, K, N, M);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+#ifndef JJO_SKINNY_RT
+#define JJO_SKINNY_RT 2
+#endif
+#ifndef JJO_SKINNY_P
+#define JJO_SKINNY_P 2
+#endif
+
+bool gemm_skinny_supported(const void *w, const void *xq, int K, int M) {
+    return K % 256 == 0 && M >= 1 && M <= kSkinnyMaxBatch && ((uintptr_t)w & 15) == 0 && ((uintptr_t)xq & 15) == 0;
+}
+
+hipError_t launch_gemm_skinny(const void *w, const void *xq, float *y, int K, int N, int M, hipStream_t stream) {
+    if (!gemm_skinny_supported(w, xq, K, M)) return hipErrorInvalidValue;
+    if (M <= 16) return launch_rcp<JJO_SKINNY_RT, 1, JJO_SKINNY_P>(w, xq, y, K, N, M, stream);
+    return launch_rcp<JJO_SKINNY_RT, 2, JJO_SKINNY_P>(w, xq, y, K, N, M, stream);
+}
+
+}  // namespace jjo

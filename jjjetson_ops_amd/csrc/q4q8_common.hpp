@@ -37,6 +37,10 @@ hipError_t launch_gemv_dot4(const void *w, const void *xq, float *y, int K, int 
 // launch_quantize_q8_1); xq_out (nullable) receives the Q8_1 bytes.
 hipError_t launch_gemv_fused(const void *w, const float *x, void *xq_out, float *y, int K, int N,
                              hipStream_t stream);
+// Batch <= 32: int8 MFMA 16x16 tiles, weights streamed per wave, K split over 4 waves.
+bool gemm_skinny_supported(const void *w, const void *xq, int K, int M);
+hipError_t launch_gemm_skinny(const void *w, const void *xq, float *y, int K, int N, int M,
+                              hipStream_t stream);
 hipError_t launch_gemm_mfma(const void *w, const void *xq, float *y, int K, int N, int M,
                             hipStream_t stream);
 hipError_t launch_gemm_mfma_grouped(const void *w, const void *xq, const int32_t *expert_offsets,
@@ -49,5 +53,9 @@ hipError_t launch_block_sums(const void *w, const void *xq, int32_t *sumi, int K
 // (K is cut into at most 4 slices of 4096 values).
 constexpr int kGemvMaxBatch = 8;
 constexpr int kGemvMaxK = 4 * 4096;
+constexpr int kSkinnyMaxBatch = 32;
+// AUTO dispatch: the GEMV up to this batch, the skinny MFMA kernel above it (up to
+// kSkinnyMaxBatch), the tiled MFMA GEMM beyond (measured crossovers at K=4096).
+constexpr int kGemvPreferredBatch = 4;
 
 }  // namespace jjo

@@ -154,6 +154,28 @@ def test_gemm_mfma(K, N, M, dev):
     np.testing.assert_allclose(got, c_oracle.matmul(w, xq, K, N, M), rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("M", [1, 3, 4, 8, 13, 16, 17, 32])
+@pytest.mark.parametrize("K,N", [(4096, 257), (11008, 64), (256, 5), (768, 96), (14336, 48), (512, 33)])
+def test_gemm_skinny(K, N, M, dev):
+    note(f"gemm skinny K={K} N={N} M={M}")
+    w = make_w(N, K, 11 * N + K)
+    x = make_x(K, M, 300 + M)
+    xq = c_oracle.quantize_q8_1(x, [K, M])
+    got = run_mm(w, xq, K, N, M, capi.ALGO_SKINNY, dev)
+    np.testing.assert_allclose(got, c_oracle.matmul(w, xq, K, N, M), rtol=RTOL, atol=ATOL)
+
+
+def test_gemm_skinny_rejects_unsupported(dev):
+    """K % 256 != 0 and batch > 32 are refused with an error, not computed."""
+    import torch
+    for K, M in ((640, 4), (4096, 33)):
+        w = torch.zeros(8 * K // 32 * 18, dtype=torch.uint8, device=dev)
+        xq = torch.zeros(M * K // 128 * 144, dtype=torch.uint8, device=dev)
+        y = torch.empty(M * 8, dtype=torch.float32, device=dev)
+        with pytest.raises(RuntimeError, match="skinny"):
+            capi.mat_mul(w, xq, y, K, 8, M, algo=capi.ALGO_SKINNY)
+
+
 @pytest.mark.parametrize("K,N", [(4096, 11008), (11008, 4096), (128, 33), (640, 257), (4096, 5)])
 def test_fused_quantize_gemv(K, N, dev):
     """mat_mul_q4_0_q8_1_f32_device at batch 1: the in-kernel quantization writes the
