@@ -21,16 +21,20 @@
 //     no barrier inside the K loop.  The K-slice partials are added through LDS in
 //     slice order at the end.
 //   * K positions inside a block are permuted consistently for both operands: MFMA
-//     k-group g (lanes 16g..16g+15) takes elements 8g..8g+7, i.e. 8 contiguous
-//     activation bytes, and the weight nibbles of bytes 8(g&1)..8(g&1)+7, low
-//     nibbles for g < 2 and high nibbles for g >= 2.
+//     k-group g (lanes 16g..16g+15) takes the nibble byte dword g of the Q4_0 block,
+//     i.e. elements 4g..4g+3 (low nibbles) and 16+4g..16+4g+3 (high nibbles), and
+//     activation dwords g and g+4 (one ds_read2_b32).
 //   * The MFMA accumulator starts at 0x4B400000 (the bits of 1.5*2^23), so the
 //     result read as fp32 is 1.5*2^23 + sumi exactly and the epilogue needs no
-//     convert:
+//     convert; two VALU ops per element and block:
 //         t = fma(D, d_x/8, -1.5*2^23 * d_x/8)     (= round(sumi*d_x)/8)
-//         acc += d_w * (t - s_x)                    (= d_w*(sumi*d_x - 8*s_x)/8)
-//     The (d_x/8, -1.5*2^23*d_x/8, s_x) triples of a stage are converted once per
-//     stage into a wave-private LDS table.
+//         acc += d_w * t                            (v_fma_mix: d_w stays fp16)
+//     The (d_x/8, -1.5*2^23*d_x/8) pairs of a stage are converted once per stage
+//     into a wave-private LDS table.
+//   * The -8*s_x term, sum_b d_w[n,b]*s_x[m,b], is itself a contraction over the
+//     blocks: one v_mfma_f32_16x16x16_f16 per stage and tile adds -d_w*s_x for the
+//     stage's 8 blocks into the same accumulator (fp16 x fp16 products are exact
+//     in fp32).  y = 8*acc.
 //
 // Requirements (checked by the launcher): K % 256 == 0, w and xq 16-byte aligned.
 #include <hip/hip_fp16.h>
@@ -42,7 +46,7 @@ namespace {
 
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kWaves = 4;  // K-slices per workgroup
@@ -76,7 +80,7 @@ struct Geo {
     static constexpr int kXBytes = 2 * kQ8BlockBytes * 16 * CT;      // 288 * 16 * CT (max M)
     static constexpr int kXInstrMax = (kXBytes / 16 + 63) / 64;
     static constexpr int kStageBytes = kWBytes + kXBytes;
-    static constexpr int kScBytes = kStageBlocks * 3 * 16 * CT * 4;   // dx8, nb8, sx per block/token
+    static constexpr int kScBytes = kStageBlocks * 2 * 16 * CT * 4;   // dx8, nb8 per block/token
 };
 
 template <int RT, int CT, int P>
@@ -86,6 +90,13 @@ struct Lds {
     static constexpr int kRedBytes = kWaves * RT * CT * 64 * 16;
     static_assert(kRedBytes <= kBytes, "reduction area must fit the rings");
 };
+
+#ifdef JJO_SKINNY_TRACE
+__device__ unsigned long long g_skinny_trace[4096 * 4][16];
+#define TR(i) if (lane == 0 && blockIdx.x < 4096) g_skinny_trace[blockIdx.x * 4 + wave][i] = __builtin_amdgcn_s_memrealtime()
+#else
+#define TR(i)
+#endif
 
 template <int RT, int CT, int P>
 __global__ __launch_bounds__(64 * kWaves) void gemm_skinny_kernel(const uint8_t *__restrict__ w,
@@ -161,84 +172,104 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_skinny_kernel(const uint8_t 
         for (int ct = 0; ct < CT; ++ct) acc[rt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // token rows this lane feeds to the MFMA (clamped: rows >= M are never stored)
-    int a_tok_off[CT];
+    int a_tok_row[CT], a_tok_off[CT];
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct) a_tok_off[ct] = min(16 * ct + l16, M - 1) * kQ8BlockBytes + 16 + 8 * g;
-    const int w_lane_off = l16 * kStageRowBytes + 2 + 8 * (g & 1);
-    const int w_shift = 4 * (g >> 1);
+    for (int ct = 0; ct < CT; ++ct) {
+        a_tok_row[ct] = min(16 * ct + l16, M - 1) * kQ8BlockBytes;
+        a_tok_off[ct] = a_tok_row[ct] + 16 + 4 * g;
+    }
 
     auto consume = [&](int s) {
         const uint8_t *st = ring + (s % P) * G::kStageBytes;
         const uint8_t *xs = st + G::kWBytes;
-        // activation scales of the stage -> sc[b][{dx8,nb8,sx}][token]
+        // activation scales of the stage -> sc[b][{dx8, nb8}][token]
         if (lane < 32 * CT) {
             const int m = lane & (16 * CT - 1), h = lane / (16 * CT);
-            const uint32_t *ds = reinterpret_cast<const uint32_t *>(xs + h * kQ8BlockBytes * M +
-                                                                    min(m, M - 1) * kQ8BlockBytes);
-            const uint4 v = *reinterpret_cast<const uint4 *>(ds);
+            const uint4 v = *reinterpret_cast<const uint4 *>(xs + h * kQ8BlockBytes * M + min(m, M - 1) * kQ8BlockBytes);
             const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const float dx8 = __half2float(__ushort_as_half((unsigned short)(vv[j] & 0xffffu))) * 0.125f;
-                const float sx = __half2float(__ushort_as_half((unsigned short)(vv[j] >> 16)));
-                float *row = sc + (4 * h + j) * 3 * 16 * CT;
+                float *row = sc + (4 * h + j) * 2 * 16 * CT;
                 row[m] = dx8;
                 row[16 * CT + m] = -kBias * dx8;
-                row[32 * CT + m] = sx;
             }
+        }
+        // -s_x of the stage's 8 blocks as the f16 A operand of the s_x MFMA: lane
+        // (token l16, group g < 2) holds blocks 4g..4g+3; groups 2, 3 are zero.
+        f16x4 sx_op[CT];
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(xs + (g & 1) * kQ8BlockBytes * M + a_tok_row[ct]);
+            const uint32_t keep = g < 2 ? 0xffffffffu : 0u;
+            const uint32_t lo = (__builtin_amdgcn_perm(v.y, v.x, 0x07060302u) ^ 0x80008000u) & keep;
+            const uint32_t hi = (__builtin_amdgcn_perm(v.w, v.z, 0x07060302u) ^ 0x80008000u) & keep;
+            sx_op[ct] = __builtin_bit_cast(f16x4, (uint64_t)hi << 32 | lo);
+        }
+        // d_w of blocks 4(g&1)..4(g&1)+3 of this lane's weight row: the B operand of the s_x MFMA
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            const _Float16 *dr = reinterpret_cast<const _Float16 *>(st + (rt * 16 + l16) * kStageRowBytes +
+                                                                    (g & 1) * 4 * kQ4BlockBytes);
+            f16x4 dw_op;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dw_op[j] = dr[j * kQ4BlockBytes / 2];
+#pragma unroll
+            for (int ct = 0; ct < CT; ++ct)
+                acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(sx_op[ct], dw_op, acc[rt][ct], 0, 0, 0);
         }
 #pragma unroll
         for (int bb = 0; bb < kStageBlocks; ++bb) {
             const int h = bb >> 2, j = bb & 3;
             long aop[CT];
-            f32x4 dx8[CT], nb8[CT], sx[CT];
+            f32x4 dx8[CT], nb8[CT];
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct) {
-                aop[ct] = *reinterpret_cast<const long *>(xs + h * kQ8BlockBytes * M + a_tok_off[ct] + 32 * j);
-                const float *row = sc + bb * 3 * 16 * CT + 16 * ct + 4 * g;
+                // activation dwords g and g+4 of the block: elements 4g..4g+3 and 16+4g..16+4g+3
+                const uint32_t *qa =
+                    reinterpret_cast<const uint32_t *>(xs + h * kQ8BlockBytes * M + a_tok_off[ct] + 32 * j);
+                aop[ct] = (long)((uint64_t)qa[4] << 32 | qa[0]);
+                const float *row = sc + bb * 2 * 16 * CT + 16 * ct + 4 * g;
                 dx8[ct] = *reinterpret_cast<const f32x4 *>(row);
                 nb8[ct] = *reinterpret_cast<const f32x4 *>(row + 16 * CT);
-                sx[ct] = *reinterpret_cast<const f32x4 *>(row + 32 * CT);
             }
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) {
-                const uint8_t *wr = st + rt * 16 * kStageRowBytes + bb * kQ4BlockBytes;
-                uint32_t q0, q1;
-                if ((bb & 1) == 0) {  // nibbles at 2 mod 4: re-align three dwords
-                    const uint32_t *p = reinterpret_cast<const uint32_t *>(wr + w_lane_off - 2);
-                    const uint32_t d0 = p[0], d1 = p[1], d2 = p[2];
-                    q0 = __builtin_amdgcn_alignbyte(d1, d0, 2);
-                    q1 = __builtin_amdgcn_alignbyte(d2, d1, 2);
+                const uint8_t *wr = st + (rt * 16 + l16) * kStageRowBytes + bb * kQ4BlockBytes;
+                uint32_t q;
+                if ((bb & 1) == 0) {  // nibble dword g at 2 mod 4: re-align
+                    const uint32_t *p = reinterpret_cast<const uint32_t *>(wr + 4 * g);
+                    q = __builtin_amdgcn_alignbyte(p[1], p[0], 2);
                 } else {
-                    const uint32_t *p = reinterpret_cast<const uint32_t *>(wr + w_lane_off);
-                    q0 = p[0];
-                    q1 = p[1];
+                    q = *reinterpret_cast<const uint32_t *>(wr + 2 + 4 * g);
                 }
-                const float dw = __half2float(
-                    __ushort_as_half(*reinterpret_cast<const unsigned short *>(wr + l16 * kStageRowBytes)));
-                const long bop =
-                    (long)(((uint64_t)((q1 >> w_shift) & 0x0f0f0f0fu) << 32) | ((q0 >> w_shift) & 0x0f0f0f0fu));
+                const _Float16 dw = *reinterpret_cast<const _Float16 *>(wr);
+                const long bop = (long)((uint64_t)((q >> 4) & 0x0f0f0f0fu) << 32 | (q & 0x0f0f0f0fu));
 #pragma unroll
                 for (int ct = 0; ct < CT; ++ct) {
                     const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop[ct], bop, bias, 0, 0, 0);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const float t = fmaf(__int_as_float(d[i]), dx8[ct][i], nb8[ct][i]);
-                        acc[rt][ct][i] = fmaf(dw, t - sx[ct][i], acc[rt][ct][i]);
+                        acc[rt][ct][i] = fmaf((float)dw, t, acc[rt][ct][i]);
                     }
                 }
             }
         }
     };
 
+    TR(0);
     if (n_my > 0) {
         const int pre = min(P, n_my);
         for (int s = 0; s < pre; ++s) issue(s);
+        TR(1);
         for (int s = 0; s < n_my; ++s) {
             const int ahead = min(P, n_my - s) - 1;  // stages issued after s
             vm_wait(ahead * per_stage);
             __builtin_amdgcn_sched_barrier(0);
+            if (s < 6) { TR(2 + 2 * s); }
             consume(s);
+            if (s < 6) { TR(3 + 2 * s); }
             __builtin_amdgcn_sched_barrier(0);
             if (s + P < n_my) {
                 JJO_LGKM0();  // slot s % P fully read before it is refilled
@@ -249,6 +280,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_skinny_kernel(const uint8_t 
     }
 
     // K-slice partials -> LDS (over the rings), summed in slice order by wave 0.
+    TR(14);
     __syncthreads();
     f32x4 *red = reinterpret_cast<f32x4 *>(smem);
 #pragma unroll
@@ -274,6 +306,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_skinny_kernel(const uint8_t 
                 }
             }
     }
+    TR(15);
 }
 
 template <int RT, int CT, int P>
@@ -303,4 +336,9 @@ hipError_t launch_gemm_skinny(const void *w, const void *xq, float *y, int K, in
     return launch_rcp<JJO_SKINNY_RT, 2, JJO_SKINNY_P>(w, xq, y, K, N, M, stream);
 }
 
+#ifdef JJO_SKINNY_TRACE
+extern "C" int jjo_skinny_trace(void *host, size_t bytes) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_skinny_trace), bytes, 0, hipMemcpyDeviceToHost);
+}
+#endif
 }  // namespace jjo
