@@ -9,8 +9,9 @@
 // weight rows as its columns, so one MFMA = 16 tokens x 16 weight rows x one 32-wide
 // K block, and an output lane holds four tokens of ONE weight row (one d_w per lane).
 //
-//   * Workgroup = 4 waves = 4 K-slices of the same RT*16 weight rows.  Each wave
-//     streams its slice through its own LDS ring of P stages; a stage is 8 K blocks:
+//   * Workgroup = 4 waves = 4 interleaved K-slices of the same RT*16 weight rows
+//     (wave w takes stages w, w+4, ...).  Each wave streams its slice through its
+//     own LDS ring of P stages; a stage is 8 K blocks:
 //       weights:     RT*16 rows x 144 B (8 Q4_0 blocks), row-major, 144 B per row
 //       activation:  the 2 Q8_1 superblocks of the stage for all M tokens, copied as
 //                    the one contiguous 288*M-byte run they occupy in the
@@ -115,10 +116,10 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_skinny_kernel(const uint8_t 
     const size_t row_bytes = (size_t)nb * kQ4BlockBytes;
     const int n0 = blockIdx.x * (16 * RT);
 
-    // K-slice of this wave, in stages
-    const int per = (n_stages + kWaves - 1) / kWaves;
-    const int s_beg = min(n_stages, wave * per);
-    const int n_my = min(n_stages, s_beg + per) - s_beg;
+    // Stages of this wave: wave, wave + 4, wave + 8, ...  The 4 waves of the
+    // workgroup read adjacent 144-byte pieces of the same rows at the same time,
+    // 576 contiguous bytes per row, which keeps HBM pages and L2 lines shared.
+    const int n_my = (n_stages - wave + kWaves - 1) / kWaves;
 
     uint8_t *ring = smem + wave * L::kWaveBytes;
     float *sc = reinterpret_cast<float *>(ring + P * G::kStageBytes);
@@ -142,7 +143,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_skinny_kernel(const uint8_t 
 
     auto issue = [&](int s) {  // stage s of this wave's slice into slot s % P
         uint8_t *st = ring + (s % P) * G::kStageBytes;
-        const int gs = s_beg + s;
+        const int gs = wave + kWaves * s;
         const uint8_t *ws = w_base + (size_t)gs * kStageRowBytes;
 #pragma unroll
         for (int i = 0; i < G::kWInstr; ++i) {

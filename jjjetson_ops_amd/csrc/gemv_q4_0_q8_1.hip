@@ -394,9 +394,15 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
 // Row groups per workgroup (the activation staging of a workgroup is shared by
 // its RG row groups of U rows).  Single-token decode favours wide workgroups of
 // short row groups; multi-token batches favour four row groups of four rows.
+#ifndef JJO_GEMV1_RG1
+#define JJO_GEMV1_RG1 8
+#endif
+#ifndef JJO_GEMV1_U
+#define JJO_GEMV1_U 2
+#endif
 template <int M, int JS>
 constexpr int rg_for() {
-    if (M == 1) return JS == 1 ? 8 : JS == 2 ? 4 : JS == 3 ? 4 : 2;
+    if (M == 1) return JS == 1 ? JJO_GEMV1_RG1 : JS == 2 ? 4 : JS == 3 ? 4 : 2;
     return JS == 1 ? 4 : JS == 2 ? 2 : 1;
 }
 
@@ -449,7 +455,7 @@ hipError_t launch_m(const void *w, const void *xin, uint8_t *xq_out, float *y, i
 hipError_t launch_gemv_dot4(const void *w, const void *xq, float *y, int K, int N, int M,
                             hipStream_t stream) {
     switch (M) {
-        case 1: return launch_m<1, 2, false>(w, xq, nullptr, y, K, N, stream);
+        case 1: return launch_m<1, JJO_GEMV1_U, false>(w, xq, nullptr, y, K, N, stream);
         case 2: return launch_m<2, 4, false>(w, xq, nullptr, y, K, N, stream);
         case 3: return launch_m<3, 4, false>(w, xq, nullptr, y, K, N, stream);
         case 4: return launch_m<4, 4, false>(w, xq, nullptr, y, K, N, stream);
@@ -463,7 +469,7 @@ hipError_t launch_gemv_dot4(const void *w, const void *xq, float *y, int K, int 
 
 hipError_t launch_gemv_fused(const void *w, const float *x, void *xq_out, float *y, int K, int N,
                              hipStream_t stream) {
-    return launch_m<1, 2, true>(w, x, (uint8_t *)xq_out, y, K, N, stream);
+    return launch_m<1, JJO_GEMV1_U, true>(w, x, (uint8_t *)xq_out, y, K, N, stream);
 }
 
 }  // namespace jjo
