@@ -236,7 +236,23 @@ def cpu_baseline(M, K, N, budget_s=10.0):
             break
     out["numpy"] = {"value": wbytes / (el2 / n2) / 1e9, "unit": "GB/s", "blas_threads": blas_threads,
                     "ms_per_step": el2 / n2 * 1e3, "steps": n2}
-    out["host"] = {"cpu_count": os.cpu_count(), "model": _cpu_model()}
+    # torch-CPU fp32 x @ dequant(W).T (the dense float path a CPU engine would run).
+    import torch
+    from jjjetson_ops_amd import q4_0
+    wf = torch.from_numpy(q4_0.dequantize_q4_0_np(w, N, K))
+    xt = torch.from_numpy(x)
+    n3 = 0
+    t0 = time.perf_counter()
+    while True:
+        xt @ wf.T
+        n3 += 1
+        el3 = time.perf_counter() - t0
+        if el3 > budget_s / 4 or n3 >= 2000:
+            break
+    out["torch_fp32"] = {"value": wbytes / (el3 / n3) / 1e9, "unit": "GB/s (Q4_0-equivalent weight bytes)",
+                         "threads": torch.get_num_threads(), "ms_per_step": el3 / n3 * 1e3, "steps": n3,
+                         "what": "x @ dequant(W).T in fp32 on torch CPU"}
+    out["host"] = {"cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(), "model": _cpu_model()}
     return out
 
 

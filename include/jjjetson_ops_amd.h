@@ -152,6 +152,103 @@ int mat_mul_q4_0_q8_1_grouped_device(const void *d_w_q4_0, const void *d_x_q8_1,
                                      const int32_t *d_route_dst, float *d_y, int ncols_k,
                                      int nrows_out, int n_routes, void *stream);
 
+/*
+ * Engine linear layer with Q4_0 weights: the slot beside linear_forward_device
+ * (src/cuda/linear.h:7-9, called from src/engine/transformer_runner.cpp:214-216,294,
+ * 319-327).  Same argument order as the reference with the cuBLAS handle slot
+ * replaced by the Q8_1 workspace:
+ *   input   fp32 [num_tokens][in_features] (features fastest, the engine's layout)
+ *   weight  Q4_0 [out_features][in_features/32] blocks
+ *   output  fp32 [num_tokens][out_features]
+ *   quant_workspace  linear_q4_0_workspace_bytes(in_features, num_tokens) bytes of
+ *            device memory (may be NULL when num_tokens == 1: the decode step runs
+ *            as one fused quantize+GEMV launch).
+ * in_features must be a multiple of 128.  No allocation, asynchronous on `stream`.
+ */
+int64_t linear_q4_0_workspace_bytes(int in_features, int num_tokens);
+int linear_q4_0_forward_device(void *stream, void *quant_workspace, const float *input,
+                               const void *weight_q4_0, float *output, int in_features,
+                               int out_features, int num_tokens);
+
+/*
+ * Host-buffer test wrapper around linear_q4_0_forward_device, in the argument order
+ * of linear_forward_host (src/cuda/linear.h:12-13).  Synchronous.
+ */
+int linear_q4_0_forward_host(float *input, const void *weight_q4_0, float *output, int in_features,
+                             int num_tokens, int out_features);
+
+/* ------------------------------------------------------------------ MoE FFN
+ * The Q4_0 replacement of the reference's MoE pipeline
+ * (moe_pipeline_sota_forward_device, src/cuda/moe/moe_pipeline_sota.cu:163-198):
+ * top-k -> dispatch -> grouped gate/up -> SwiGLU -> grouped down -> combine,
+ * with Q4_0 expert weights and Q8_1 activations.  Routes are r = t*top_k + k.
+ * Expert weights: w_gate, w_up Q4_0 [E][I][H/32]; w_down Q4_0 [E][H][I/32].
+ */
+
+/*
+ * Top-k gating.  Replaces moe_top_k_launch_cuda (src/cuda/moe/moe_top_k.cu:218):
+ * ids[t*top_k + k] = the k-th largest logit's expert (smaller id on ties),
+ * weights = softmax over the top_k selected logits.  logits fp32 [T][E].
+ * 1 <= top_k <= min(32, E), E <= 1024.
+ */
+int moe_top_k_device(void *stream, const float *logits, float *route_weights, int32_t *expert_ids,
+                     int num_tokens, int num_experts, int top_k);
+
+/*
+ * Dispatch.  Replaces moe_dispatch_sota_launch_cuda
+ * (src/cuda/moe/moe_dispatch_sota.cu:113-151): a stable sort of the routes by
+ * expert.  expert_offsets[E+1]; src_route[p] = the route at permuted row p
+ * (the reference's expanded_src_for_dest_row; token = src_route[p] / top_k);
+ * dst_of_route[r] = its permuted row (the reference's inv_permuted_idx,
+ * moe_combine_sota.cu:6-19).  Instead of permuting fp32 rows, x_q8_1_permuted
+ * receives the Q8_1 blocks of x_q8_1 (quantizer layout over T tokens, hidden_size
+ * values) in permuted order (quantizer layout over T*top_k rows).  The two Q8_1
+ * pointers may both be NULL (routing tables only).
+ */
+int moe_dispatch_q8_1_device(void *stream, const int32_t *expert_ids, const void *x_q8_1, int num_tokens,
+                             int top_k, int hidden_size, int num_experts, int32_t *expert_offsets,
+                             int32_t *src_route, int32_t *dst_of_route, void *x_q8_1_permuted);
+
+/*
+ * Grouped gate|up projection of the permuted rows in one launch: gate_up[p][0:I]
+ * = w_gate[e(p)] . x_p, gate_up[p][I:2I] = w_up[e(p)] . x_p (fp32 [R][2I]).
+ * Replaces the first two moe_grouped_gemm_nt calls
+ * (src/cuda/moe/moe_pipeline_sota.cu:181-184).  intermediate_size % 128 == 0.
+ */
+int moe_q4_0_gate_up_device(void *stream, const void *w_gate, const void *w_up, const void *x_q8_1_permuted,
+                            const int32_t *expert_offsets, int num_experts, float *gate_up, int hidden_size,
+                            int intermediate_size, int n_routes);
+
+/*
+ * SwiGLU fused with the Q8_1 quantizer: mid = silu(gate) * up
+ * (swiglu_silu_mul_launch_device, src/cuda/swiglu.cu:5-28) on gate_up [rows][2I],
+ * quantized to Q8_1 (quantizer layout over `rows` tokens, I values) for the down
+ * projection.  mid_f32 (optional, may be NULL) receives the fp32 mid values.
+ */
+int swiglu_quantize_q8_1_device(void *stream, const float *gate_up, void *mid_q8_1, float *mid_f32,
+                                int rows, int intermediate_size);
+
+/*
+ * Combine.  Replaces moe_combine_sota_launch_cuda
+ * (src/cuda/moe/moe_combine_sota.cu:58-66): y[t][h] = sum_k w[t,k] *
+ * expert_out[dst_of_route[t*top_k+k]][h], summed in k order.  hidden_size % 4 == 0.
+ */
+int moe_combine_device(void *stream, const float *expert_out, const int32_t *dst_of_route,
+                       const float *route_weights, float *y, int num_tokens, int hidden_size, int top_k);
+
+/*
+ * The whole Q4_0 MoE FFN on device pointers: x fp32 [T][H], logits fp32 [T][E],
+ * y fp32 [T][H].  `workspace` (256-byte aligned) holds every intermediate; its
+ * size is moe_q4_0_ffn_workspace_bytes(...).  Eight launches, no allocation,
+ * asynchronous on `stream`.  H % 128 == 0, I % 128 == 0.
+ */
+int64_t moe_q4_0_ffn_workspace_bytes(int num_tokens, int hidden_size, int intermediate_size, int num_experts,
+                                     int top_k);
+int moe_q4_0_ffn_forward_device(void *stream, const float *x, const float *logits, const void *w_gate,
+                                const void *w_up, const void *w_down, float *y, int num_tokens, int hidden_size,
+                                int intermediate_size, int num_experts, int top_k, void *workspace,
+                                int64_t workspace_bytes);
+
 #ifdef __cplusplus
 }
 #endif

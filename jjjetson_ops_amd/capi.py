@@ -42,6 +42,16 @@ EXPORTED_SYMBOLS = (
     "mat_mul_q4_0_q8_1_device_algo",
     "mat_mul_q4_0_q8_1_block_sums_device",
     "mat_mul_q4_0_q8_1_grouped_device",
+    "linear_q4_0_workspace_bytes",
+    "linear_q4_0_forward_device",
+    "linear_q4_0_forward_host",
+    "moe_top_k_device",
+    "moe_dispatch_q8_1_device",
+    "moe_q4_0_gate_up_device",
+    "swiglu_quantize_q8_1_device",
+    "moe_combine_device",
+    "moe_q4_0_ffn_workspace_bytes",
+    "moe_q4_0_ffn_forward_device",
 )
 
 
@@ -89,6 +99,26 @@ def lib() -> ctypes.CDLL:
         L.mat_mul_q4_0_q8_1_block_sums_device.argtypes = [vp, vp, vp, i32, i32, i32, vp]
         L.mat_mul_q4_0_q8_1_grouped_device.restype = i32
         L.mat_mul_q4_0_q8_1_grouped_device.argtypes = [vp, vp, vp, i32, vp, vp, i32, i32, i32, vp]
+        L.linear_q4_0_workspace_bytes.restype = i64
+        L.linear_q4_0_workspace_bytes.argtypes = [i32, i32]
+        L.linear_q4_0_forward_device.restype = i32
+        L.linear_q4_0_forward_device.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32]
+        L.linear_q4_0_forward_host.restype = i32
+        L.linear_q4_0_forward_host.argtypes = [vp, vp, vp, i32, i32, i32]
+        L.moe_top_k_device.restype = i32
+        L.moe_top_k_device.argtypes = [vp, vp, vp, vp, i32, i32, i32]
+        L.moe_dispatch_q8_1_device.restype = i32
+        L.moe_dispatch_q8_1_device.argtypes = [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp]
+        L.moe_q4_0_gate_up_device.restype = i32
+        L.moe_q4_0_gate_up_device.argtypes = [vp, vp, vp, vp, vp, i32, vp, i32, i32, i32]
+        L.swiglu_quantize_q8_1_device.restype = i32
+        L.swiglu_quantize_q8_1_device.argtypes = [vp, vp, vp, vp, i32, i32]
+        L.moe_combine_device.restype = i32
+        L.moe_combine_device.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32]
+        L.moe_q4_0_ffn_workspace_bytes.restype = i64
+        L.moe_q4_0_ffn_workspace_bytes.argtypes = [i32, i32, i32, i32, i32]
+        L.moe_q4_0_ffn_forward_device.restype = i32
+        L.moe_q4_0_ffn_forward_device.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp, i64]
         _lib = L
     return _lib
 
@@ -213,3 +243,64 @@ def parse_q8_1(raw, n_blocks: int):
     s = np.empty((n_blocks, 4), np.float32)
     lib().parse_q8_1_output(raw.ctypes.data, qs.ctypes.data, d.ctypes.data, s.ctypes.data, n_blocks)
     return qs, d, s
+
+
+# ---------------------------------------------------------------- engine linear
+def linear_q4_0(x, w, y, in_features: int, out_features: int, num_tokens: int, ws=None, stream=None) -> None:
+    """linear_q4_0_forward_device: y [T, out] = x [T, in] . dequant(w [out, in/32 blocks]).T"""
+    _check(lib().linear_q4_0_forward_device(_stream(stream), None if ws is None else _dev(ws, "ws"), _dev(x, "x"),
+                                            _dev(w, "w"), _dev(y, "y"), in_features, out_features, num_tokens),
+           "linear_q4_0_forward_device")
+
+
+def linear_q4_0_workspace_bytes(in_features: int, num_tokens: int) -> int:
+    return int(lib().linear_q4_0_workspace_bytes(in_features, num_tokens))
+
+
+# ---------------------------------------------------------------- MoE FFN
+def moe_top_k(logits, weights, ids, num_tokens: int, num_experts: int, top_k: int, stream=None) -> None:
+    _check(lib().moe_top_k_device(_stream(stream), _dev(logits, "logits"), _dev(weights, "weights"),
+                                  _dev(ids, "ids"), num_tokens, num_experts, top_k), "moe_top_k_device")
+
+
+def moe_dispatch(ids, offsets, src_route, dst_of_route, num_tokens: int, top_k: int, hidden: int,
+                 num_experts: int, xq=None, xq_perm=None, stream=None) -> None:
+    _check(lib().moe_dispatch_q8_1_device(_stream(stream), _dev(ids, "ids"), None if xq is None else _dev(xq, "xq"),
+                                          num_tokens, top_k, hidden, num_experts, _dev(offsets, "offsets"),
+                                          _dev(src_route, "src_route"), _dev(dst_of_route, "dst_of_route"),
+                                          None if xq_perm is None else _dev(xq_perm, "xq_perm")),
+           "moe_dispatch_q8_1_device")
+
+
+def moe_gate_up(w_gate, w_up, xq_perm, offsets, num_experts: int, gate_up, hidden: int, inter: int,
+                n_routes: int, stream=None) -> None:
+    _check(lib().moe_q4_0_gate_up_device(_stream(stream), _dev(w_gate, "w_gate"), _dev(w_up, "w_up"),
+                                         _dev(xq_perm, "xq_perm"), _dev(offsets, "offsets"), num_experts,
+                                         _dev(gate_up, "gate_up"), hidden, inter, n_routes),
+           "moe_q4_0_gate_up_device")
+
+
+def swiglu_quantize(gate_up, mid_q, rows: int, inter: int, mid_f32=None, stream=None) -> None:
+    _check(lib().swiglu_quantize_q8_1_device(_stream(stream), _dev(gate_up, "gate_up"), _dev(mid_q, "mid_q"),
+                                             None if mid_f32 is None else _dev(mid_f32, "mid_f32"), rows, inter),
+           "swiglu_quantize_q8_1_device")
+
+
+def moe_combine(expert_out, dst_of_route, weights, y, num_tokens: int, hidden: int, top_k: int,
+                stream=None) -> None:
+    _check(lib().moe_combine_device(_stream(stream), _dev(expert_out, "expert_out"),
+                                    _dev(dst_of_route, "dst_of_route"), _dev(weights, "weights"), _dev(y, "y"),
+                                    num_tokens, hidden, top_k), "moe_combine_device")
+
+
+def moe_ffn_workspace_bytes(num_tokens: int, hidden: int, inter: int, num_experts: int, top_k: int) -> int:
+    return int(lib().moe_q4_0_ffn_workspace_bytes(num_tokens, hidden, inter, num_experts, top_k))
+
+
+def moe_ffn(x, logits, w_gate, w_up, w_down, y, num_tokens: int, hidden: int, inter: int, num_experts: int,
+            top_k: int, ws, stream=None) -> None:
+    _check(lib().moe_q4_0_ffn_forward_device(_stream(stream), _dev(x, "x"), _dev(logits, "logits"),
+                                             _dev(w_gate, "w_gate"), _dev(w_up, "w_up"), _dev(w_down, "w_down"),
+                                             _dev(y, "y"), num_tokens, hidden, inter, num_experts, top_k,
+                                             _dev(ws, "ws"), ws.numel() * ws.element_size()),
+           "moe_q4_0_ffn_forward_device")

@@ -378,4 +378,247 @@ int mat_mul_q4_0_q8_1(const void *weight_q4_0, const float *input, uint8_t *quan
     return rc;
 }
 
+// ---------------------------------------------------------------- engine linear
+int64_t linear_q4_0_workspace_bytes(int in_features, int num_tokens) {
+    if (in_features <= 0 || num_tokens <= 0 || in_features % kQSuper != 0) return -1;
+    return (int64_t)num_tokens * (in_features / kQSuper) * kQ8BlockBytes;
+}
+
+int linear_q4_0_forward_device(void *stream, void *quant_workspace, const float *input,
+                               const void *weight_q4_0, float *output, int in_features,
+                               int out_features, int num_tokens) {
+    clear_error();
+    if (in_features <= 0 || out_features <= 0 || num_tokens <= 0)
+        return set_error(JJO_ERR_INVALID_ARG, "linear_q4_0: invalid in_features=%d out_features=%d num_tokens=%d",
+                         in_features, out_features, num_tokens);
+    if (input == nullptr || weight_q4_0 == nullptr || output == nullptr)
+        return set_error(JJO_ERR_INVALID_ARG, "linear_q4_0: null pointer argument");
+    return mat_mul_q4_0_q8_1_f32_device(weight_q4_0, input, quant_workspace, output, in_features, out_features,
+                                        num_tokens, stream);
+}
+
+int linear_q4_0_forward_host(float *input, const void *weight_q4_0, float *output, int in_features,
+                             int num_tokens, int out_features) {
+    clear_error();
+    const int64_t ws_bytes = linear_q4_0_workspace_bytes(in_features, num_tokens);
+    if (ws_bytes < 0 || out_features <= 0)
+        return set_error(JJO_ERR_INVALID_ARG, "linear_q4_0: invalid in_features=%d out_features=%d num_tokens=%d",
+                         in_features, out_features, num_tokens);
+    if (input == nullptr || weight_q4_0 == nullptr || output == nullptr)
+        return set_error(JJO_ERR_INVALID_ARG, "linear_q4_0: null pointer argument");
+    int rc = require_gfx950();
+    if (rc != JJO_OK) return rc;
+    const int64_t n_in = (int64_t)in_features * num_tokens;
+    const int64_t w_bytes = (int64_t)out_features * (in_features / kQK) * kQ4BlockBytes;
+    const int64_t y_elems = (int64_t)out_features * num_tokens;
+    hipStream_t s = nullptr;
+    void *dw = nullptr, *dq = nullptr;
+    float *dx = nullptr, *dy = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamCreateWithFlags");
+    do {
+        if ((e = hipMalloc((void **)&dx, n_in * sizeof(float))) != hipSuccess) { rc = hip_fail(e, "hipMalloc(x)"); break; }
+        if ((e = hipMalloc(&dq, ws_bytes)) != hipSuccess) { rc = hip_fail(e, "hipMalloc(ws)"); break; }
+        if ((e = hipMalloc(&dw, w_bytes)) != hipSuccess) { rc = hip_fail(e, "hipMalloc(w)"); break; }
+        if ((e = hipMalloc((void **)&dy, y_elems * sizeof(float))) != hipSuccess) { rc = hip_fail(e, "hipMalloc(y)"); break; }
+        if ((e = hipMemcpyAsync(dx, input, n_in * sizeof(float), hipMemcpyHostToDevice, s)) != hipSuccess) { rc = hip_fail(e, "H2D x"); break; }
+        if ((e = hipMemcpyAsync(dw, weight_q4_0, w_bytes, hipMemcpyHostToDevice, s)) != hipSuccess) { rc = hip_fail(e, "H2D w"); break; }
+        if ((rc = linear_q4_0_forward_device(s, dq, dx, dw, dy, in_features, out_features, num_tokens)) != JJO_OK) break;
+        if ((e = hipMemcpyAsync(output, dy, y_elems * sizeof(float), hipMemcpyDeviceToHost, s)) != hipSuccess) { rc = hip_fail(e, "D2H y"); break; }
+        if ((e = hipStreamSynchronize(s)) != hipSuccess) { rc = hip_fail(e, "hipStreamSynchronize"); break; }
+    } while (0);
+    if (dx) (void)hipFree(dx);
+    if (dq) (void)hipFree(dq);
+    if (dw) (void)hipFree(dw);
+    if (dy) (void)hipFree(dy);
+    (void)hipStreamDestroy(s);
+    return rc;
+}
+
+// ---------------------------------------------------------------- MoE FFN (Q4_0 experts)
+namespace {
+int check_moe_shape(int num_tokens, int hidden, int inter, int num_experts, int top_k) {
+    if (num_tokens <= 0 || hidden <= 0 || inter <= 0)
+        return set_error(JJO_ERR_INVALID_ARG, "moe: invalid num_tokens=%d hidden=%d intermediate=%d", num_tokens,
+                         hidden, inter);
+    if (hidden % kQSuper != 0 || inter % kQSuper != 0)
+        return set_error(JJO_ERR_INVALID_ARG, "moe: hidden_size and intermediate_size must be multiples of %d",
+                         kQSuper);
+    if (num_experts <= 0 || num_experts > 1024 || top_k <= 0 || top_k > 32 || top_k > num_experts)
+        return set_error(JJO_ERR_INVALID_ARG, "moe: need 1 <= top_k <= min(32, num_experts), num_experts <= 1024 "
+                         "(got top_k=%d num_experts=%d)", top_k, num_experts);
+    if ((int64_t)num_tokens * top_k > 0x7fffffffLL / 4)
+        return set_error(JJO_ERR_INVALID_ARG, "moe: too many routes");
+    return JJO_OK;
+}
+
+struct MoeWs {
+    float *route_w;
+    int32_t *ids, *offsets, *src_route, *dst_of_route;
+    uint8_t *xq, *xp, *midq;
+    float *gate_up, *eout;
+    int64_t bytes;
+};
+
+// Workspace carve-up, every part 256-byte aligned.
+MoeWs moe_ws_layout(uint8_t *base, int T, int H, int I, int E, int top_k) {
+    const int64_t R = (int64_t)T * top_k;
+    int64_t off = 0;
+    auto take = [&](int64_t bytes) {
+        uint8_t *p = base ? base + off : nullptr;
+        off += (bytes + 255) / 256 * 256;
+        return p;
+    };
+    MoeWs w{};
+    w.route_w = (float *)take(R * 4);
+    w.ids = (int32_t *)take(R * 4);
+    w.offsets = (int32_t *)take((int64_t)(E + 1) * 4);
+    w.src_route = (int32_t *)take(R * 4);
+    w.dst_of_route = (int32_t *)take(R * 4);
+    w.xq = take((int64_t)T * (H / kQSuper) * kQ8BlockBytes);
+    w.xp = take(R * (H / kQSuper) * kQ8BlockBytes);
+    w.gate_up = (float *)take(R * 2 * I * 4);
+    w.midq = take(R * (I / kQSuper) * kQ8BlockBytes);
+    w.eout = (float *)take(R * H * 4);
+    w.bytes = off;
+    return w;
+}
+}  // namespace
+
+int moe_top_k_device(void *stream, const float *logits, float *route_weights, int32_t *expert_ids,
+                     int num_tokens, int num_experts, int top_k) {
+    clear_error();
+    int rc = check_moe_shape(num_tokens, kQSuper, kQSuper, num_experts, top_k);
+    if (rc != JJO_OK) return rc;
+    if (logits == nullptr || route_weights == nullptr || expert_ids == nullptr)
+        return set_error(JJO_ERR_INVALID_ARG, "moe_top_k: null pointer argument");
+    if ((rc = require_gfx950()) != JJO_OK) return rc;
+    hipError_t e = launch_moe_top_k(logits, route_weights, expert_ids, num_tokens, num_experts, top_k,
+                                    (hipStream_t)stream);
+    return e == hipSuccess ? JJO_OK : hip_fail(e, "moe_top_k launch");
+}
+
+int moe_dispatch_q8_1_device(void *stream, const int32_t *expert_ids, const void *x_q8_1, int num_tokens,
+                             int top_k, int hidden_size, int num_experts, int32_t *expert_offsets,
+                             int32_t *src_route, int32_t *dst_of_route, void *x_q8_1_permuted) {
+    clear_error();
+    int rc = check_moe_shape(num_tokens, hidden_size, kQSuper, num_experts, top_k);
+    if (rc != JJO_OK) return rc;
+    if (expert_ids == nullptr || expert_offsets == nullptr || src_route == nullptr || dst_of_route == nullptr)
+        return set_error(JJO_ERR_INVALID_ARG, "moe_dispatch: null pointer argument");
+    if ((x_q8_1 == nullptr) != (x_q8_1_permuted == nullptr))
+        return set_error(JJO_ERR_INVALID_ARG, "moe_dispatch: give both Q8_1 buffers or neither");
+    if (x_q8_1 != nullptr && (!aligned(x_q8_1, 16) || !aligned(x_q8_1_permuted, 16)))
+        return set_error(JJO_ERR_INVALID_ARG, "moe_dispatch: Q8_1 buffers must be 16-byte aligned");
+    if ((rc = require_gfx950()) != JJO_OK) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    const int R = num_tokens * top_k;
+    hipError_t e = launch_moe_dispatch(expert_ids, R, num_experts, expert_offsets, src_route, dst_of_route, s);
+    if (e != hipSuccess) return hip_fail(e, "moe_dispatch launch");
+    if (x_q8_1 != nullptr) {
+        e = launch_moe_gather_q8_1(x_q8_1, src_route, x_q8_1_permuted, num_tokens, R, top_k, hidden_size, s);
+        if (e != hipSuccess) return hip_fail(e, "moe_gather_q8_1 launch");
+    }
+    return JJO_OK;
+}
+
+int swiglu_quantize_q8_1_device(void *stream, const float *gate_up, void *mid_q8_1, float *mid_f32,
+                                int rows, int intermediate_size) {
+    clear_error();
+    if (rows <= 0 || intermediate_size <= 0 || intermediate_size % kQSuper != 0)
+        return set_error(JJO_ERR_INVALID_ARG, "swiglu_quantize: rows > 0 and intermediate_size %% %d == 0 required",
+                         kQSuper);
+    if (gate_up == nullptr || mid_q8_1 == nullptr || !aligned(gate_up, 16) || !aligned(mid_q8_1, 16) ||
+        (mid_f32 != nullptr && !aligned(mid_f32, 16)))
+        return set_error(JJO_ERR_INVALID_ARG, "swiglu_quantize: non-null 16-byte aligned buffers required");
+    int rc = require_gfx950();
+    if (rc != JJO_OK) return rc;
+    hipError_t e = launch_swiglu_quantize_q8_1(gate_up, mid_q8_1, mid_f32, intermediate_size, rows,
+                                               (hipStream_t)stream);
+    return e == hipSuccess ? JJO_OK : hip_fail(e, "swiglu_quantize launch");
+}
+
+int moe_q4_0_gate_up_device(void *stream, const void *w_gate, const void *w_up, const void *x_q8_1_permuted,
+                            const int32_t *expert_offsets, int num_experts, float *gate_up, int hidden_size,
+                            int intermediate_size, int n_routes) {
+    clear_error();
+    int rc = validate_mm(w_gate, x_q8_1_permuted, gate_up, hidden_size, 2 * intermediate_size, n_routes);
+    if (rc != JJO_OK) return rc;
+    if (w_up == nullptr || !aligned(w_up, 4) || expert_offsets == nullptr || num_experts <= 0 ||
+        num_experts > 4096)
+        return set_error(JJO_ERR_INVALID_ARG, "moe_gate_up: bad w_up / expert_offsets / num_experts");
+    if (intermediate_size % 128 != 0)
+        return set_error(JJO_ERR_INVALID_ARG, "moe_gate_up: intermediate_size must be a multiple of 128");
+    if ((rc = require_gfx950()) != JJO_OK) return rc;
+    hipError_t e = launch_gemm_mfma_grouped(w_gate, x_q8_1_permuted, expert_offsets, num_experts, nullptr, gate_up,
+                                            hidden_size, 2 * intermediate_size, n_routes, (hipStream_t)stream, w_up,
+                                            intermediate_size);
+    return e == hipSuccess ? JJO_OK : hip_fail(e, "moe_gate_up launch");
+}
+
+int moe_combine_device(void *stream, const float *expert_out, const int32_t *dst_of_route,
+                       const float *route_weights, float *y, int num_tokens, int hidden_size, int top_k) {
+    clear_error();
+    if (num_tokens <= 0 || hidden_size <= 0 || hidden_size % 4 != 0 || top_k <= 0)
+        return set_error(JJO_ERR_INVALID_ARG, "moe_combine: num_tokens, top_k > 0 and hidden_size %% 4 == 0");
+    if (expert_out == nullptr || dst_of_route == nullptr || route_weights == nullptr || y == nullptr ||
+        !aligned(expert_out, 16) || !aligned(y, 16))
+        return set_error(JJO_ERR_INVALID_ARG, "moe_combine: non-null buffers, 16-byte aligned expert_out and y");
+    int rc = require_gfx950();
+    if (rc != JJO_OK) return rc;
+    hipError_t e = launch_moe_combine(expert_out, dst_of_route, route_weights, y, num_tokens, hidden_size, top_k,
+                                      (hipStream_t)stream);
+    return e == hipSuccess ? JJO_OK : hip_fail(e, "moe_combine launch");
+}
+
+int64_t moe_q4_0_ffn_workspace_bytes(int num_tokens, int hidden_size, int intermediate_size, int num_experts,
+                                     int top_k) {
+    if (check_moe_shape(num_tokens, hidden_size, intermediate_size, num_experts, top_k) != JJO_OK) return -1;
+    return moe_ws_layout(nullptr, num_tokens, hidden_size, intermediate_size, num_experts, top_k).bytes;
+}
+
+int moe_q4_0_ffn_forward_device(void *stream, const float *x, const float *logits, const void *w_gate,
+                                const void *w_up, const void *w_down, float *y, int num_tokens, int hidden_size,
+                                int intermediate_size, int num_experts, int top_k, void *workspace,
+                                int64_t workspace_bytes) {
+    clear_error();
+    const int T = num_tokens, H = hidden_size, I = intermediate_size, E = num_experts;
+    int rc = check_moe_shape(T, H, I, E, top_k);
+    if (rc != JJO_OK) return rc;
+    if (x == nullptr || logits == nullptr || w_gate == nullptr || w_up == nullptr || w_down == nullptr ||
+        y == nullptr || workspace == nullptr)
+        return set_error(JJO_ERR_INVALID_ARG, "moe_ffn: null pointer argument");
+    if (!aligned(x, 16) || !aligned(y, 16) || !aligned(workspace, 256) || !aligned(w_gate, 4) ||
+        !aligned(w_up, 4) || !aligned(w_down, 4))
+        return set_error(JJO_ERR_INVALID_ARG, "moe_ffn: x, y 16-byte, workspace 256-byte, weights 4-byte aligned");
+    const MoeWs ws = moe_ws_layout((uint8_t *)workspace, T, H, I, E, top_k);
+    if (workspace_bytes < ws.bytes)
+        return set_error(JJO_ERR_INVALID_ARG, "moe_ffn: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
+                         (long long)ws.bytes);
+    if ((rc = require_gfx950()) != JJO_OK) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    const int R = T * top_k;
+    hipError_t e;
+    // 1) x -> Q8_1 (once per token), 2) top-k gating, 3) stable dispatch + Q8_1 row gather
+    if ((e = launch_quantize_q8_1(x, ws.xq, H, T, 1, s)) != hipSuccess) return hip_fail(e, "moe_ffn quantize x");
+    if ((e = launch_moe_top_k(logits, ws.route_w, ws.ids, T, E, top_k, s)) != hipSuccess)
+        return hip_fail(e, "moe_ffn top_k");
+    if ((e = launch_moe_dispatch(ws.ids, R, E, ws.offsets, ws.src_route, ws.dst_of_route, s)) != hipSuccess)
+        return hip_fail(e, "moe_ffn dispatch");
+    if ((e = launch_moe_gather_q8_1(ws.xq, ws.src_route, ws.xp, T, R, top_k, H, s)) != hipSuccess)
+        return hip_fail(e, "moe_ffn gather");
+    // 4) gate|up of every route's expert in one grouped launch, 5) SwiGLU + Q8_1
+    if ((e = launch_gemm_mfma_grouped(w_gate, ws.xp, ws.offsets, E, nullptr, ws.gate_up, H, 2 * I, R, s, w_up, I)) !=
+        hipSuccess)
+        return hip_fail(e, "moe_ffn gate_up");
+    if ((e = launch_swiglu_quantize_q8_1(ws.gate_up, ws.midq, nullptr, I, R, s)) != hipSuccess)
+        return hip_fail(e, "moe_ffn swiglu_quantize");
+    // 6) down projection, 7) weighted combine back to token order
+    if ((e = launch_gemm_mfma_grouped(w_down, ws.midq, ws.offsets, E, nullptr, ws.eout, I, H, R, s)) != hipSuccess)
+        return hip_fail(e, "moe_ffn down");
+    if ((e = launch_moe_combine(ws.eout, ws.dst_of_route, ws.route_w, y, T, H, top_k, s)) != hipSuccess)
+        return hip_fail(e, "moe_ffn combine");
+    return JJO_OK;
+}
+
 }  // extern "C"

@@ -99,7 +99,7 @@ template <bool kGrouped>
 __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     const uint8_t *__restrict__ w_all, const uint8_t *__restrict__ xq, float *__restrict__ y, int K,
     int N, int M, const int32_t *__restrict__ expert_offsets, int n_experts,
-    const int32_t *__restrict__ route_dst) {
+    const int32_t *__restrict__ route_dst, const uint8_t *__restrict__ w2, int n_split) {
     extern __shared__ __align__(16) uint8_t smem[];
 
     const int tid = threadIdx.x;
@@ -118,6 +118,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     // ---- token range of this workgroup ----
     int m0, m_end;
     const uint8_t *w = w_all;
+    int expert = 0;
     if constexpr (kGrouped) {
         // Tile t of the concatenated per-expert tile lists.
         int t = blockIdx.y;
@@ -135,7 +136,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
             t -= tiles;
         }
         if (m0 < 0) return;  // uniform over the workgroup
-        w = w_all + (size_t)e * N * row_bytes;
+        expert = e;
+        w = w_all + (size_t)e * (w2 != nullptr ? n_split : N) * row_bytes;
     } else {
         m0 = blockIdx.y * BM;
         m_end = M;
@@ -144,7 +146,20 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     // ---- staging: weights through registers, activations by LDS DMA ----
     const int st_row = tid >> 1;    // W: one row, one block pair per thread
     const int st_half = tid & 1;
-    const uint8_t *w_src = w + (size_t)min(n0 + st_row, N - 1) * row_bytes + (size_t)st_half * 36;
+    // Two stacked matrices (w2 != nullptr): rows [0, n_split) from w, rows
+    // [n_split, N) from w2 (expert e's block of each); n_split % BN == 0, so a
+    // workgroup's rows come from one of them.
+    int n_loc0 = n0, n_mat = N;
+    if (w2 != nullptr) {
+        if (n0 < n_split) {
+            n_mat = n_split;
+        } else {
+            w = w2 + (size_t)expert * (N - n_split) * row_bytes;
+            n_loc0 = n0 - n_split;
+            n_mat = N - n_split;
+        }
+    }
+    const uint8_t *w_src = w + (size_t)min(n_loc0 + st_row, n_mat - 1) * row_bytes + (size_t)st_half * 36;
     uint32_t wst[9];                // this thread's 2 raw Q4_0 blocks (36 bytes)
 
     auto load_w = [&](int c) {
@@ -230,6 +245,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
 
     // Columns past m_end hold stale LDS bytes: their scales are forced to zero.
     const bool col_ok[2] = {m0 + wm * 64 + l32 < m_end, m0 + wm * 64 + 32 + l32 < m_end};
+    const bool ct_live[2] = {m0 + wm * 64 < m_end, m0 + wm * 64 + 32 < m_end};  // wave-uniform
 
     // Pipeline, one barrier per stage: while stage c is computed from buffers c&1,
     // the loads of stage c+1 are in flight; stage c+1's weights are unpacked into the
@@ -260,6 +276,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
             hdr[ct][2] = col_ok[ct] ? h.z : 0u; hdr[ct][3] = col_ok[ct] ? h.w : 0u;
         }
 
+        // Token sub-tiles past the last valid token (grouped tails) skip the math:
+        // wave-uniform branches.
+        if (!ct_live[0]) goto stage_done;
 #pragma unroll
         for (int b = 0; b < KB; ++b) {
             i32x4 bop[2], aop[2];
@@ -291,14 +310,21 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
             }
             // Two result tiles in flight: the MFMA of the next tile overlaps the
             // VALU epilogue of the previous one.
-            i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[0], bop[0], bias, 0, 0, 0);
-            i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[0], bop[1], bias, 0, 0, 0);
-            epilogue(acc[0][0], d0, wv[0], dx8[0], nb8[0]);
-            d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[1], bop[0], bias, 0, 0, 0);
-            epilogue(acc[0][1], d1, wv[0], dx8[1], nb8[1]);
-            d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[1], bop[1], bias, 0, 0, 0);
-            epilogue(acc[1][0], d0, wv[1], dx8[0], nb8[0]);
-            epilogue(acc[1][1], d1, wv[1], dx8[1], nb8[1]);
+            if (ct_live[1]) {
+                i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[0], bop[0], bias, 0, 0, 0);
+                i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[0], bop[1], bias, 0, 0, 0);
+                epilogue(acc[0][0], d0, wv[0], dx8[0], nb8[0]);
+                d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[1], bop[0], bias, 0, 0, 0);
+                epilogue(acc[0][1], d1, wv[0], dx8[1], nb8[1]);
+                d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[1], bop[1], bias, 0, 0, 0);
+                epilogue(acc[1][0], d0, wv[1], dx8[0], nb8[0]);
+                epilogue(acc[1][1], d1, wv[1], dx8[1], nb8[1]);
+            } else {
+                const i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[0], bop[0], bias, 0, 0, 0);
+                const i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[1], bop[0], bias, 0, 0, 0);
+                epilogue(acc[0][0], d0, wv[0], dx8[0], nb8[0]);
+                epilogue(acc[1][0], d1, wv[1], dx8[0], nb8[0]);
+            }
         }
 
         // sum_b d_w * (-s_x) over this stage's 4 blocks on the f16 MFMA (K = 8:
@@ -326,6 +352,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
                     acc[rt][ct] = __builtin_amdgcn_mfma_f32_32x32x8f16(aop[rt], bop[ct], acc[rt][ct], 0, 0, 0);
         }
 
+    stage_done:
         if (c + 1 < n_stages) {
             store_w((c + 1) & 1);  // waits for W(c+1) and X(c+1), issued a compute phase ago
             __syncthreads();
@@ -388,13 +415,14 @@ hipError_t launch_gemm_mfma(const void *w, const void *xq, float *y, int K, int 
     if (e != hipSuccess) return e;
     const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
     hipLaunchKernelGGL(gemm_q4_0_q8_1_mfma_kernel<false>, grid, dim3(kThreads), kSmemBytes, stream,
-                       (const uint8_t *)w, (const uint8_t *)xq, y, K, N, M, nullptr, 0, nullptr);
+                       (const uint8_t *)w, (const uint8_t *)xq, y, K, N, M, nullptr, 0, nullptr,
+                       (const uint8_t *)nullptr, 0);
     return hipGetLastError();
 }
 
 hipError_t launch_gemm_mfma_grouped(const void *w, const void *xq, const int32_t *expert_offsets,
                                     int n_experts, const int32_t *route_dst, float *y, int K,
-                                    int N, int n_routes, hipStream_t stream) {
+                                    int N, int n_routes, hipStream_t stream, const void *w2, int n_split) {
     hipError_t e = set_smem_attr<true>();
     if (e != hipSuccess) return e;
     // Upper bound on the number of token tiles over all experts.
@@ -402,7 +430,7 @@ hipError_t launch_gemm_mfma_grouped(const void *w, const void *xq, const int32_t
     const dim3 grid((N + BN - 1) / BN, max_tiles);
     hipLaunchKernelGGL(gemm_q4_0_q8_1_mfma_kernel<true>, grid, dim3(kThreads), kSmemBytes, stream,
                        (const uint8_t *)w, (const uint8_t *)xq, y, K, N, n_routes, expert_offsets,
-                       n_experts, route_dst);
+                       n_experts, route_dst, (const uint8_t *)w2, n_split);
     return hipGetLastError();
 }
 

@@ -1,0 +1,212 @@
+// MoE routing around the Q4_0 expert GEMMs on gfx950: top-k gating, dispatch
+// (stable sort of routes by expert plus the permuted Q8_1 activation rows) and
+// combine.  Semantics follow the reference's moe_top_k / moe_dispatch_sota /
+// moe_combine_sota kernels; the data movement is redesigned for this path:
+//   * dispatch gathers Q8_1 blocks (1.125 B per value) instead of fp32 rows: the
+//     activation is quantized once per token, before the permutation, which gives
+//     the same bytes as quantizing the permuted rows (quantization is per row);
+//   * the route sort is a counting sort in one workgroup (16 waves, each owning a
+//     contiguous range of routes; ranks inside a wave come from ballots), which is
+//     stable exactly like the reference's radix sort.
+#include <hip/hip_runtime.h>
+
+#include "q4q8_common.hpp"
+
+namespace jjo {
+namespace {
+
+// ---------------------------------------------------------------- top-k
+// One lane per token (num_experts <= 1024, top_k <= 32).
+// Selection: moe_top_k.cu:120-176 -- top_k rounds, each takes the largest
+// remaining logit, the smaller expert id on ties; ids[k] in selection order.
+// Weights: softmax over the selected logits (delayed_softmax, moe_top_k.cu:12-55,
+// 190-195): max = the first selected value, e_i = expf(v_i - max), and the sum is
+// the 32-lane xor butterfly of warp_reduce_xor_sum (include/cuda_utils.cuh:37-43)
+// over e_0..e_{top_k-1} placed in lanes 0..top_k-1 (zeros elsewhere), so the
+// association order is the reference's; w_i = e_i * (1 / sum).
+__global__ __launch_bounds__(64) void moe_top_k_kernel(const float *__restrict__ logits,
+                                                       float *__restrict__ weights, int *__restrict__ ids,
+                                                       int num_tokens, int num_experts, int top_k) {
+    const int t = blockIdx.x * 64 + threadIdx.x;
+    if (t >= num_tokens) return;
+    const float *row = logits + (size_t)t * num_experts;
+    float sel[32];
+    int sel_id[32];
+    for (int k = 0; k < top_k; ++k) {
+        float best = -INFINITY;
+        int best_id = -1;
+        for (int e = 0; e < num_experts; ++e) {
+            bool taken = false;
+            for (int j = 0; j < k; ++j) taken |= (sel_id[j] == e);
+            const float v = taken ? -INFINITY : row[e];
+            if (best_id < 0 || v > best) {  // strict: the first (smallest) id wins ties
+                best = v;
+                best_id = e;
+            }
+        }
+        sel[k] = best;
+        sel_id[k] = best_id;
+    }
+    float lanes[32];
+#pragma unroll
+    for (int l = 0; l < 32; ++l) lanes[l] = 0.0f;
+    const float mx = sel[0];
+    for (int k = 0; k < top_k; ++k) lanes[k] = expf(sel[k] - mx);
+    float tree[32];
+#pragma unroll
+    for (int l = 0; l < 32; ++l) tree[l] = lanes[l];
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) {
+        float nx[32];
+#pragma unroll
+        for (int l = 0; l < 32; ++l) nx[l] = tree[l] + tree[l ^ off];
+#pragma unroll
+        for (int l = 0; l < 32; ++l) tree[l] = nx[l];
+    }
+    const float inv_sum = 1.0f / tree[0];
+    for (int k = 0; k < top_k; ++k) {
+        weights[(size_t)t * top_k + k] = lanes[k] * inv_sum;
+        ids[(size_t)t * top_k + k] = sel_id[k];
+    }
+}
+
+// ---------------------------------------------------------------- dispatch
+// Route r = t*top_k + k has expert ids[r].  Output position of r:
+//   pos(r) = #{routes with a smaller expert} + #{r' < r with the same expert}
+// (a stable sort by expert, as cub::DeviceRadixSort::SortPairs over the arange in
+// moe_dispatch_sota.cu:127-136), and expert_offsets[e] = #{routes with expert < e}
+// (the lower-bound search of moe_dispatch_sota.cu:45-71).
+constexpr int kDispatchWaves = 16;
+
+__device__ __forceinline__ uint64_t ballot64(bool p) { return __ballot(p); }
+
+__global__ __launch_bounds__(64 * kDispatchWaves) void moe_dispatch_kernel(
+    const int *__restrict__ ids, int num_routes, int num_experts, int32_t *__restrict__ expert_offsets,
+    int32_t *__restrict__ src_route, int32_t *__restrict__ dst_of_route) {
+    extern __shared__ int32_t cnt[];  // [kDispatchWaves][num_experts]
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int per = (num_routes + kDispatchWaves - 1) / kDispatchWaves;
+    const int r_beg = min(num_routes, wave * per);
+    const int r_end = min(num_routes, r_beg + per);
+    int32_t *my = cnt + wave * num_experts;
+
+    for (int e = threadIdx.x; e < kDispatchWaves * num_experts; e += blockDim.x) cnt[e] = 0;
+    __syncthreads();
+    // per-wave histogram of its route range
+    // (out-of-range ids are clamped to a valid expert: memory safety, not semantics)
+    for (int r = r_beg + lane; r < r_end; r += 64) atomicAdd(&my[min(max(ids[r], 0), num_experts - 1)], 1);
+    __syncthreads();
+    // exclusive scan over (expert, wave): base of wave w for expert e
+    if (threadIdx.x == 0) {
+        int run = 0;
+        for (int e = 0; e < num_experts; ++e) {
+            expert_offsets[e] = run;
+            for (int w = 0; w < kDispatchWaves; ++w) {
+                const int c = cnt[w * num_experts + e];
+                cnt[w * num_experts + e] = run;
+                run += c;
+            }
+        }
+        expert_offsets[num_experts] = run;
+    }
+    __syncthreads();
+    // stable placement: 64 routes per step in route order; lanes with equal experts
+    // are ranked by lane index through a ballot per distinct expert of the step
+    for (int r0 = r_beg; r0 < r_end; r0 += 64) {
+        const int r = r0 + lane;
+        const bool live = r < r_end;
+        const int e = live ? min(max(ids[r], 0), num_experts - 1) : -1;
+        uint64_t todo = ballot64(live);
+        int pos = 0;
+        while (todo != 0) {
+            const int leader = __builtin_ctzll(todo);
+            const int el = __shfl(e, leader);
+            const uint64_t grp = ballot64(live && e == el);
+            if (e == el && live) pos = my[el] + __builtin_popcountll(grp & ((1ull << lane) - 1ull));
+            if (lane == leader) my[el] += __builtin_popcountll(grp);
+            todo &= ~grp;
+        }
+        if (live) {
+            src_route[pos] = r;
+            dst_of_route[r] = pos;
+        }
+    }
+}
+
+// Permuted Q8_1 activation: block (s * n_routes + p) <- block (s * num_tokens + token(p))
+// with token(p) = src_route[p] / top_k (moe_dispatch_sota.cu:73-95 on Q8_1 blocks).
+__global__ __launch_bounds__(256) void moe_gather_q8_1_kernel(const uint8_t *__restrict__ xq,
+                                                              const int32_t *__restrict__ src_route,
+                                                              uint8_t *__restrict__ xp, int num_tokens,
+                                                              int n_routes, int top_k, int n_super) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 16-byte piece
+    const int64_t total = (int64_t)n_super * n_routes * (kQ8BlockBytes / 16);
+    if (i >= total) return;
+    const int piece = (int)(i % (kQ8BlockBytes / 16));
+    const int64_t blk = i / (kQ8BlockBytes / 16);
+    const int p = (int)(blk % n_routes);
+    const int64_t s = blk / n_routes;
+    const int t = min(src_route[p] / top_k, num_tokens - 1);
+    const uint4 v = *reinterpret_cast<const uint4 *>(xq + (s * num_tokens + t) * kQ8BlockBytes + 16 * piece);
+    *reinterpret_cast<uint4 *>(xp + blk * kQ8BlockBytes + 16 * piece) = v;
+}
+
+// ---------------------------------------------------------------- combine
+// y[t][h] = sum over k in order of w[t,k] * expert_out[dst(t,k)][h], acc from 0
+// (moe_combine_sota.cu:21-41).  Four consecutive h per thread.
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float *__restrict__ expert_out,
+                                                          const int32_t *__restrict__ dst_of_route,
+                                                          const float *__restrict__ route_weights,
+                                                          float *__restrict__ y, int hidden, int top_k) {
+    const int t = blockIdx.y;
+    const int h = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (h >= hidden) return;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = 0; k < top_k; ++k) {
+        const int r = t * top_k + k;
+        const float w = route_weights[r];
+        const float4 v = *reinterpret_cast<const float4 *>(expert_out + (size_t)dst_of_route[r] * hidden + h);
+        acc.x = fmaf(w, v.x, acc.x);
+        acc.y = fmaf(w, v.y, acc.y);
+        acc.z = fmaf(w, v.z, acc.z);
+        acc.w = fmaf(w, v.w, acc.w);
+    }
+    *reinterpret_cast<float4 *>(y + (size_t)t * hidden + h) = acc;
+}
+
+}  // namespace
+
+hipError_t launch_moe_top_k(const float *logits, float *weights, int *ids, int num_tokens, int num_experts,
+                            int top_k, hipStream_t stream) {
+    hipLaunchKernelGGL(moe_top_k_kernel, dim3((num_tokens + 63) / 64), dim3(64), 0, stream, logits, weights, ids,
+                       num_tokens, num_experts, top_k);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_dispatch(const int *ids, int num_routes, int num_experts, int32_t *expert_offsets,
+                               int32_t *src_route, int32_t *dst_of_route, hipStream_t stream) {
+    const size_t smem = (size_t)kDispatchWaves * num_experts * sizeof(int32_t);
+    hipLaunchKernelGGL(moe_dispatch_kernel, dim3(1), dim3(64 * kDispatchWaves), smem, stream, ids, num_routes,
+                       num_experts, expert_offsets, src_route, dst_of_route);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_gather_q8_1(const void *xq, const int32_t *src_route, void *xp, int num_tokens, int n_routes,
+                                  int top_k, int K, hipStream_t stream) {
+    const int n_super = K / kQSuper;
+    const int64_t total = (int64_t)n_super * n_routes * (kQ8BlockBytes / 16);
+    hipLaunchKernelGGL(moe_gather_q8_1_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
+                       (const uint8_t *)xq, src_route, (uint8_t *)xp, num_tokens, n_routes, top_k, n_super);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_combine(const float *expert_out, const int32_t *dst_of_route, const float *route_weights,
+                              float *y, int num_tokens, int hidden, int top_k, hipStream_t stream) {
+    const dim3 grid((unsigned)((hidden / 4 + 255) / 256), (unsigned)num_tokens);
+    hipLaunchKernelGGL(moe_combine_kernel, grid, dim3(256), 0, stream, expert_out, dst_of_route, route_weights, y,
+                       hidden, top_k);
+    return hipGetLastError();
+}
+
+}  // namespace jjo

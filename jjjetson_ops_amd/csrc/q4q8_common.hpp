@@ -45,7 +45,18 @@ hipError_t launch_gemm_mfma(const void *w, const void *xq, float *y, int K, int 
                             hipStream_t stream);
 hipError_t launch_gemm_mfma_grouped(const void *w, const void *xq, const int32_t *expert_offsets,
                                     int n_experts, const int32_t *route_dst, float *y, int K,
-                                    int N, int n_routes, hipStream_t stream);
+                                    int N, int n_routes, hipStream_t stream, const void *w2 = nullptr,
+                                    int n_split = 0);
+hipError_t launch_swiglu_quantize_q8_1(const float *gate_up, void *y, float *mid_out, int64_t K, int64_t rows,
+                                       hipStream_t stream);
+hipError_t launch_moe_top_k(const float *logits, float *weights, int *ids, int num_tokens, int num_experts,
+                            int top_k, hipStream_t stream);
+hipError_t launch_moe_dispatch(const int *ids, int num_routes, int num_experts, int32_t *expert_offsets,
+                               int32_t *src_route, int32_t *dst_of_route, hipStream_t stream);
+hipError_t launch_moe_gather_q8_1(const void *xq, const int32_t *src_route, void *xp, int num_tokens, int n_routes,
+                                  int top_k, int K, hipStream_t stream);
+hipError_t launch_moe_combine(const float *expert_out, const int32_t *dst_of_route, const float *route_weights,
+                              float *y, int num_tokens, int hidden, int top_k, hipStream_t stream);
 hipError_t launch_block_sums(const void *w, const void *xq, int32_t *sumi, int K, int N, int M,
                              hipStream_t stream);
 

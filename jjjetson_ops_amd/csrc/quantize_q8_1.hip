@@ -36,10 +36,18 @@ __device__ __forceinline__ uint32_t pack_q(float v0, float v1, float v2, float v
            ((uint32_t)(d & 0xff) << 24);
 }
 
+// silu(g) * u exactly as swiglu_silu_mul_kernel (src/cuda/swiglu.cu:5-14).
+__device__ __forceinline__ float swiglu(float g, float u) { return g * (1.0f / (1.0f + expf(-g))) * u; }
+
+// SWIGLU: the quantized value is silu(gate) * up, with gate = x[m*ldx + i] and
+// up = x[m*ldx + K + i] (the two halves of a [rows][2K] gate|up matrix);
+// mid_out (optional) receives the fp32 values.
+template <bool SWIGLU>
 __global__ __launch_bounds__(256) void quantize_q8_1_kernel(const float *__restrict__ x,
                                                             uint8_t *__restrict__ y, int64_t K,
                                                             int64_t K_pad, int64_t ne1,
-                                                            int64_t slice_blocks) {
+                                                            int64_t slice_blocks, int64_t ldx,
+                                                            float *__restrict__ mid_out) {
     const int64_t i0 = ((int64_t)blockIdx.y * 256 + threadIdx.x) * 4;  // value index in the token
     if (i0 >= K_pad) return;  // whole 32-groups leave together (K_pad % 128 == 0)
     const int64_t m = blockIdx.x;
@@ -47,7 +55,16 @@ __global__ __launch_bounds__(256) void quantize_q8_1_kernel(const float *__restr
 
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     const bool live = i0 < K;  // uniform over each 8-lane group since K % 32 == 0
-    if (live) v = *reinterpret_cast<const float4 *>(x + (z * ne1 + m) * K + i0);
+    if constexpr (SWIGLU) {
+        if (live) {
+            const float4 g = *reinterpret_cast<const float4 *>(x + m * ldx + i0);
+            const float4 u = *reinterpret_cast<const float4 *>(x + m * ldx + K + i0);
+            v = make_float4(swiglu(g.x, u.x), swiglu(g.y, u.y), swiglu(g.z, u.z), swiglu(g.w, u.w));
+            if (mid_out != nullptr) *reinterpret_cast<float4 *>(mid_out + m * K + i0) = v;
+        }
+    } else {
+        if (live) v = *reinterpret_cast<const float4 *>(x + (z * ne1 + m) * K + i0);
+    }
 
     float amax = fmaxf(fabsf(v.x), fmaxf(fabsf(v.y), fmaxf(fabsf(v.z), fabsf(v.w))));
     float sum = v.x + v.y;
@@ -90,8 +107,17 @@ hipError_t launch_quantize_q8_1(const float *x, void *y, int64_t K, int64_t ne1,
     // gridDim.y = ceil(K/512) (src/cuda/q8_1.cu:84,173).  Irrelevant when nz == 1.
     const int64_t slice_blocks = ne1 * 4 * ((K + 511) / 512);
     const dim3 grid((unsigned)ne1, (unsigned)((K_pad + 1023) / 1024), (unsigned)nz);
-    hipLaunchKernelGGL(quantize_q8_1_kernel, grid, dim3(256), 0, stream, x, (uint8_t *)y, K, K_pad,
-                       ne1, slice_blocks);
+    hipLaunchKernelGGL(quantize_q8_1_kernel<false>, grid, dim3(256), 0, stream, x, (uint8_t *)y, K, K_pad,
+                       ne1, slice_blocks, (int64_t)0, (float *)nullptr);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu_quantize_q8_1(const float *gate_up, void *y, float *mid_out, int64_t K, int64_t rows,
+                                       hipStream_t stream) {
+    const int64_t K_pad = (K + kQSuper - 1) / kQSuper * kQSuper;
+    const dim3 grid((unsigned)rows, (unsigned)((K_pad + 1023) / 1024), 1u);
+    hipLaunchKernelGGL(quantize_q8_1_kernel<true>, grid, dim3(256), 0, stream, gate_up, (uint8_t *)y, K, K_pad,
+                       rows, (int64_t)0, 2 * K, mid_out);
     return hipGetLastError();
 }
 

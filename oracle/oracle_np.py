@@ -13,6 +13,13 @@ Functions and the reference lines they follow:
 * ``block_sums``         — q4_0_q8_1_vec_dot_impl integer part, src/cuda/mm_q4_0_q8_1.cu:75-90
 * ``matmul``             — per-block epilogue :91-92 summed over K (:256-269)
 * ``quantize_q4_0``      — this build's weight generator (the reference has none)
+* ``moe_top_k``          — moe_top_k_kernel<E, false, true>, src/cuda/moe/moe_top_k.cu:120-205,
+                           softmax_warp_inplace :12-55, warp_reduce_xor_sum include/cuda_utils.cuh:37-43
+* ``moe_dispatch``       — moe_dispatch_sota_launch_cuda, src/cuda/moe/moe_dispatch_sota.cu:113-151
+                           (stable radix sort :127-136, lower-bound offsets :45-71, rows :73-95)
+* ``swiglu``             — swiglu_silu_mul_kernel, src/cuda/swiglu.cu:5-14
+* ``moe_combine``        — moe_combine_sota_unpermute_kernel, src/cuda/moe/moe_combine_sota.cu:21-41
+* ``gather_q8_1``        — the dispatch row permutation applied to Q8_1 blocks
 """
 from __future__ import annotations
 
@@ -179,3 +186,108 @@ def quantize_q4_0(wf: np.ndarray) -> np.ndarray:
 def dequantize_q4_0(w: np.ndarray, N: int, K: int) -> np.ndarray:
     nib, d = _split_w(w, N, K)
     return ((nib.astype(np.float32) - 8.0).reshape(N, K // 32, 32) * d[..., None]).reshape(N, K)
+
+
+# ---------------------------------------------------------------- MoE routing
+def _xor_butterfly_sum32(vals: np.ndarray) -> np.float32:
+    """warp_reduce_xor_sum (include/cuda_utils.cuh:37-43) over 32 float32 lanes:
+    offsets 16, 8, 4, 2, 1; lane 0's result."""
+    x = np.asarray(vals, dtype=np.float32).copy()
+    idx = np.arange(32)
+    for off in (16, 8, 4, 2, 1):
+        x = (x + x[idx ^ off]).astype(np.float32)
+    return x[0]
+
+
+def moe_top_k(logits: np.ndarray, top_k: int):
+    """ids [T, top_k] (int32) and weights [T, top_k] (float32).
+
+    Selection: top_k rounds over the remaining logits, each the largest value and
+    the smallest expert id on ties (moe_top_k.cu:120-176).  Weights: softmax over
+    the selected logits with max = the first selected, e = expf(v - max), the sum
+    as the 32-lane xor butterfly with e in lanes 0..top_k-1, w = e * (1/sum)
+    (moe_top_k.cu:12-55 with use_limit, :190-195).
+    """
+    lg = np.asarray(logits, dtype=np.float32)
+    T, E = lg.shape
+    ids = np.zeros((T, top_k), dtype=np.int32)
+    wts = np.zeros((T, top_k), dtype=np.float32)
+    for t in range(T):
+        row = lg[t].copy()
+        taken = np.zeros(E, dtype=bool)
+        sel = []
+        for k in range(top_k):
+            best, best_id = np.float32(-np.inf), -1
+            for e in range(E):
+                v = np.float32(-np.inf) if taken[e] else row[e]
+                if best_id < 0 or v > best:
+                    best, best_id = v, e
+            taken[best_id] = True
+            ids[t, k] = best_id
+            sel.append(best)
+        sel = np.array(sel, dtype=np.float32)
+        ex = np.exp((sel - sel[0]).astype(np.float32)).astype(np.float32)
+        lanes = np.zeros(32, dtype=np.float32)
+        lanes[:top_k] = ex
+        inv = np.float32(1.0) / _xor_butterfly_sum32(lanes)
+        wts[t] = (ex * inv).astype(np.float32)
+    return ids, wts
+
+
+def moe_dispatch(ids: np.ndarray, num_experts: int):
+    """Stable sort of the routes r = t*top_k + k by expert.
+
+    Returns (expert_offsets [E+1], src_route [R], dst_of_route [R]):
+    src_route[p] = route at permuted row p, dst_of_route[r] = its row
+    (moe_dispatch_sota.cu:113-151; inv_permuted_idx of moe_combine_sota.cu:6-19).
+    """
+    flat = np.asarray(ids, dtype=np.int64).reshape(-1)
+    R = flat.size
+    src = np.zeros(R, dtype=np.int32)
+    counts = np.zeros(num_experts, dtype=np.int64)
+    for e in flat:
+        counts[e] += 1
+    offsets = np.zeros(num_experts + 1, dtype=np.int32)
+    offsets[1:] = np.cumsum(counts)
+    cursor = offsets[:-1].astype(np.int64).copy()
+    for r in range(R):  # routes in increasing r: stable
+        e = flat[r]
+        src[cursor[e]] = r
+        cursor[e] += 1
+    dst = np.zeros(R, dtype=np.int32)
+    dst[src] = np.arange(R, dtype=np.int32)
+    return offsets, src, dst
+
+
+def gather_q8_1(xq: np.ndarray, src_route: np.ndarray, num_tokens: int, top_k: int, K: int) -> np.ndarray:
+    """Q8_1 blocks of the permuted rows: block (s*R + p) = block (s*T + src_route[p] // top_k)."""
+    R = src_route.size
+    blocks = np.asarray(xq, dtype=np.uint8).reshape(K // SUPER, num_tokens, BLOCK_Q8_1_BYTES)
+    return np.ascontiguousarray(blocks[:, np.asarray(src_route) // top_k, :]).reshape(-1)
+
+
+def swiglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """silu(g) * u = g * (1 / (1 + exp(-g))) * u in float32, the reference's
+    operation order (swiglu.cu:5-14)."""
+    g = np.asarray(gate, dtype=np.float32)
+    u = np.asarray(up, dtype=np.float32)
+    one = np.float32(1.0)
+    with np.errstate(over="ignore"):
+        sig = (one / (one + np.exp(-g).astype(np.float32))).astype(np.float32)
+    return ((g * sig).astype(np.float32) * u).astype(np.float32)
+
+
+def moe_combine(expert_out: np.ndarray, dst_of_route: np.ndarray, weights: np.ndarray, top_k: int) -> np.ndarray:
+    """y[t] = sum over k in order of w[t,k] * expert_out[dst(t,k)], float32, acc from 0
+    with one rounding per multiply-add (fma, moe_combine_sota.cu:31-38)."""
+    eo = np.asarray(expert_out, dtype=np.float32)
+    w = np.asarray(weights, dtype=np.float32).reshape(-1)
+    T = w.size // top_k
+    y = np.zeros((T, eo.shape[1]), dtype=np.float32)
+    for t in range(T):
+        acc = np.zeros(eo.shape[1], dtype=np.float64)
+        for k in range(top_k):
+            r = t * top_k + k
+            acc = (acc + np.float64(w[r]) * eo[dst_of_route[r]].astype(np.float64)).astype(np.float32).astype(np.float64)
+        y[t] = acc.astype(np.float32)
+    return y

@@ -1,0 +1,303 @@
+"""GPU parity of the Q4_0 MoE FFN and the engine linear, stage by stage, through
+the C ABI, against the CPU oracle.
+
+Bars:
+  * expert ids, routing tables (offsets, src_route, dst_of_route), permuted Q8_1
+    bytes, and the Q8_1 bytes of the SwiGLU output given its fp32 values: exact;
+  * top-k weights and fp32 SwiGLU values: rtol 2e-6 (expf of the GPU's libm and
+    NumPy differ by at most an ulp or two);
+  * gate/up, down and linear outputs: rtol 1e-3, atol 1e-4 against the fp64 oracle;
+  * combine: rtol 1e-6 (fp32 fma chain against fp64);
+  * end to end: the eight-launch FFN entry equals the stage-by-stage run bit for bit,
+    and the fp64 oracle chain within rtol 2e-3 / atol 2e-3 (the chain re-quantizes the
+    SwiGLU output, which the fp32/fp64 difference of the gate/up sums can move by one
+    Q8_1 step in rare elements).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from jjjetson_ops_amd import capi
+from oracle import c_oracle, oracle_np
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-3, 1e-4
+
+
+def note(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def to_dev(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def make_w(N, K, rng):
+    return c_oracle.quantize_q4_0((rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+
+
+def expert_slice(blocks_q8, off, e):
+    """Q8_1 rows [off[e], off[e+1]) of a quantizer-layout buffer of R rows, as its own buffer."""
+    return np.ascontiguousarray(blocks_q8[:, off[e]:off[e + 1], :]).reshape(-1)
+
+
+# ------------------------------------------------------------------ engine linear
+@pytest.mark.parametrize("K,N,T", [(4096, 1024, 1), (4096, 300, 7), (1024, 256, 64), (11008, 128, 1)])
+def test_linear_q4_0(K, N, T, dev):
+    import torch
+    note(f"linear_q4_0 K={K} N={N} T={T}")
+    rng = np.random.default_rng(K + N + T)
+    w = make_w(N, K, rng)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    ws = torch.empty(max(1, capi.linear_q4_0_workspace_bytes(K, T)), dtype=torch.uint8, device=dev)
+    y = torch.full((T * N,), float("nan"), dtype=torch.float32, device=dev)
+    capi.linear_q4_0(to_dev(x, dev), to_dev(w, dev), y, K, N, T, ws=ws)
+    xq = c_oracle.quantize_q8_1(x, [K, T])
+    np.testing.assert_allclose(host(y).reshape(T, N), c_oracle.matmul(w, xq, K, N, T), rtol=RTOL, atol=ATOL)
+
+
+def test_linear_q4_0_host_entry():
+    import ctypes
+    K, N, T = 512, 96, 3
+    rng = np.random.default_rng(5)
+    w = make_w(N, K, rng)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    y = np.zeros(T * N, dtype=np.float32)
+    rc = capi.lib().linear_q4_0_forward_host(x.ctypes.data, w.ctypes.data, y.ctypes.data, K, T, N)
+    assert rc == 0, capi.lib().jjo_last_error()
+    xq = c_oracle.quantize_q8_1(x, [K, T])
+    np.testing.assert_allclose(y.reshape(T, N), c_oracle.matmul(w, xq, K, N, T), rtol=RTOL, atol=ATOL)
+
+
+# ------------------------------------------------------------------ MoE stages
+MOE_CASES = [  # T, H, I, E, top_k
+    (64, 256, 384, 8, 2),
+    (5, 128, 128, 4, 1),
+    (300, 512, 256, 16, 4),
+]
+
+
+def _routing(T, E, top_k, seed, dev):
+    import torch
+    rng = np.random.default_rng(seed)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    w = torch.empty(T * top_k, dtype=torch.float32, device=dev)
+    ids = torch.empty(T * top_k, dtype=torch.int32, device=dev)
+    capi.moe_top_k(to_dev(lg, dev), w, ids, T, E, top_k)
+    return lg, host(w), host(ids)
+
+
+@pytest.mark.parametrize("T,H,I,E,top_k", MOE_CASES)
+def test_moe_top_k(T, H, I, E, top_k, dev):
+    note(f"moe_top_k T={T} E={E} k={top_k}")
+    lg, w, ids = _routing(T, E, top_k, 100 + T, dev)
+    ref_ids, ref_w = oracle_np.moe_top_k(lg, top_k)
+    assert np.array_equal(ids.reshape(T, top_k), ref_ids)
+    np.testing.assert_allclose(w.reshape(T, top_k), ref_w, rtol=2e-6, atol=1e-7)
+
+
+def test_moe_top_k_ties_take_smaller_id(dev):
+    import torch
+    note("moe_top_k ties")
+    lg = np.zeros((4, 8), dtype=np.float32)
+    lg[1, [2, 5]] = 1.0
+    lg[2] = np.float32(-3.0)
+    lg[3, 7] = 2.0
+    w = torch.empty(12, dtype=torch.float32, device=dev)
+    ids = torch.empty(12, dtype=torch.int32, device=dev)
+    capi.moe_top_k(to_dev(lg, dev), w, ids, 4, 8, 3)
+    assert host(ids).reshape(4, 3).tolist() == [[0, 1, 2], [2, 5, 0], [0, 1, 2], [7, 0, 1]]
+
+
+@pytest.mark.parametrize("T,H,I,E,top_k", MOE_CASES)
+def test_moe_dispatch_and_gather(T, H, I, E, top_k, dev):
+    import torch
+    note(f"moe_dispatch T={T} H={H} E={E} k={top_k}")
+    rng = np.random.default_rng(200 + T)
+    ids = rng.integers(0, E, size=T * top_k).astype(np.int32)
+    ids[: min(len(ids), 10)] = 0  # a crowded expert
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    xq = c_oracle.quantize_q8_1(x, [H, T])
+    R = T * top_k
+    off = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    src = torch.empty(R, dtype=torch.int32, device=dev)
+    dst = torch.empty(R, dtype=torch.int32, device=dev)
+    xp = torch.empty(R * H // 128 * 144, dtype=torch.uint8, device=dev)
+    capi.moe_dispatch(to_dev(ids, dev), off, src, dst, T, top_k, H, E, xq=to_dev(xq, dev), xq_perm=xp)
+    r_off, r_src, r_dst = oracle_np.moe_dispatch(ids, E)
+    assert np.array_equal(host(off), r_off)
+    assert np.array_equal(host(src), r_src)
+    assert np.array_equal(host(dst), r_dst)
+    assert np.array_equal(host(xp), oracle_np.gather_q8_1(xq, r_src, T, top_k, H))
+
+
+def test_moe_dispatch_large_route_count(dev):
+    """Routes spread over all 16 waves of the dispatch workgroup, several steps each."""
+    import torch
+    note("moe_dispatch R=8192 E=64")
+    rng = np.random.default_rng(3)
+    T, top_k, E = 2048, 4, 64
+    ids = rng.integers(0, E, size=T * top_k).astype(np.int32)
+    R = T * top_k
+    off = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    src = torch.empty(R, dtype=torch.int32, device=dev)
+    dst = torch.empty(R, dtype=torch.int32, device=dev)
+    capi.moe_dispatch(to_dev(ids, dev), off, src, dst, T, top_k, 128, E)
+    r_off, r_src, r_dst = oracle_np.moe_dispatch(ids, E)
+    assert np.array_equal(host(off), r_off)
+    assert np.array_equal(host(src), r_src)
+    assert np.array_equal(host(dst), r_dst)
+
+
+@pytest.mark.parametrize("T,H,I,E,top_k", MOE_CASES)
+def test_moe_gate_up(T, H, I, E, top_k, dev):
+    import torch
+    note(f"moe_gate_up T={T} H={H} I={I} E={E} k={top_k}")
+    rng = np.random.default_rng(300 + T)
+    R = T * top_k
+    ids = rng.integers(0, E, size=R).astype(np.int32)
+    off, src, _ = oracle_np.moe_dispatch(ids, E)
+    x = rng.standard_normal((R, H)).astype(np.float32)  # already-permuted rows
+    xp = c_oracle.quantize_q8_1(x, [H, R])
+    wg = [make_w(I, H, rng) for _ in range(E)]
+    wu = [make_w(I, H, rng) for _ in range(E)]
+    gu = torch.full((R * 2 * I,), float("nan"), dtype=torch.float32, device=dev)
+    capi.moe_gate_up(to_dev(np.concatenate(wg), dev), to_dev(np.concatenate(wu), dev), to_dev(xp, dev),
+                     to_dev(off, dev), E, gu, H, I, R)
+    got = host(gu).reshape(R, 2 * I)
+    blocks = xp.reshape(H // 128, R, 144)
+    for e in range(E):
+        m = off[e + 1] - off[e]
+        if m == 0:
+            continue
+        xe = expert_slice(blocks, off, e)
+        np.testing.assert_allclose(got[off[e]:off[e + 1], :I], c_oracle.matmul(wg[e], xe, H, I, m), rtol=RTOL,
+                                   atol=ATOL)
+        np.testing.assert_allclose(got[off[e]:off[e + 1], I:], c_oracle.matmul(wu[e], xe, H, I, m), rtol=RTOL,
+                                   atol=ATOL)
+
+
+@pytest.mark.parametrize("rows,I", [(64, 384), (5, 128), (300, 256)])
+def test_swiglu_quantize(rows, I, dev):
+    import torch
+    note(f"swiglu_quantize rows={rows} I={I}")
+    rng = np.random.default_rng(rows + I)
+    gu = (rng.standard_normal((rows, 2 * I)) * 3).astype(np.float32)
+    gu[0, :32] = 0.0  # an all-zero group: d = +inf as the quantizer
+    mid = torch.empty(rows * I, dtype=torch.float32, device=dev)
+    mq = torch.empty(rows * I // 128 * 144, dtype=torch.uint8, device=dev)
+    capi.swiglu_quantize(to_dev(gu, dev), mq, rows, I, mid_f32=mid)
+    mid_h = host(mid).reshape(rows, I)
+    np.testing.assert_allclose(mid_h, oracle_np.swiglu(gu[:, :I], gu[:, I:]), rtol=2e-6, atol=1e-30)
+    assert np.array_equal(host(mq), c_oracle.quantize_q8_1(mid_h, [I, rows]))
+
+
+@pytest.mark.parametrize("T,H,top_k", [(64, 256, 2), (5, 128, 1), (300, 512, 4)])
+def test_moe_combine(T, H, top_k, dev):
+    import torch
+    note(f"moe_combine T={T} H={H} k={top_k}")
+    rng = np.random.default_rng(T + H)
+    R = T * top_k
+    eo = rng.standard_normal((R, H)).astype(np.float32)
+    dst = rng.permutation(R).astype(np.int32)
+    w = rng.random(R).astype(np.float32)
+    y = torch.empty(T * H, dtype=torch.float32, device=dev)
+    capi.moe_combine(to_dev(eo, dev), to_dev(dst, dev), to_dev(w, dev), y, T, H, top_k)
+    np.testing.assert_allclose(host(y).reshape(T, H), oracle_np.moe_combine(eo, dst, w, top_k), rtol=1e-6,
+                               atol=1e-6)
+
+
+# ------------------------------------------------------------------ whole FFN
+def _ffn_inputs(T, H, I, E, seed):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    lg = rng.standard_normal((T, E)).astype(np.float32)
+    wg = [make_w(I, H, rng) for _ in range(E)]
+    wu = [make_w(I, H, rng) for _ in range(E)]
+    wd = [make_w(H, I, rng) for _ in range(E)]
+    return x, lg, wg, wu, wd
+
+
+def _oracle_ffn(x, lg, wg, wu, wd, top_k):
+    T, H = x.shape
+    I = wg[0].size * 32 // 18 // H
+    E = len(wg)
+    R = T * top_k
+    xq = c_oracle.quantize_q8_1(x, [H, T])
+    ids, w = oracle_np.moe_top_k(lg, top_k)
+    off, src, dst = oracle_np.moe_dispatch(ids, E)
+    xp = oracle_np.gather_q8_1(xq, src, T, top_k, H).reshape(H // 128, R, 144)
+    gu = np.zeros((R, 2 * I), dtype=np.float32)
+    for e in range(E):
+        m = off[e + 1] - off[e]
+        if m:
+            xe = expert_slice(xp, off, e)
+            gu[off[e]:off[e + 1], :I] = c_oracle.matmul(wg[e], xe, H, I, m)
+            gu[off[e]:off[e + 1], I:] = c_oracle.matmul(wu[e], xe, H, I, m)
+    mid = oracle_np.swiglu(gu[:, :I], gu[:, I:])
+    mq = c_oracle.quantize_q8_1(mid, [I, R]).reshape(I // 128, R, 144)
+    eo = np.zeros((R, H), dtype=np.float32)
+    for e in range(E):
+        m = off[e + 1] - off[e]
+        if m:
+            eo[off[e]:off[e + 1]] = c_oracle.matmul(wd[e], expert_slice(mq, off, e), I, H, m)
+    return oracle_np.moe_combine(eo, dst, w.reshape(-1), top_k)
+
+
+@pytest.mark.parametrize("T,H,I,E,top_k", MOE_CASES)
+def test_moe_ffn_end_to_end(T, H, I, E, top_k, dev):
+    import torch
+    note(f"moe_ffn T={T} H={H} I={I} E={E} k={top_k}")
+    x, lg, wg, wu, wd = _ffn_inputs(T, H, I, E, 400 + T)
+    d = {k: to_dev(v, dev) for k, v in dict(x=x, lg=lg, wg=np.concatenate(wg), wu=np.concatenate(wu),
+                                          wd=np.concatenate(wd)).items()}
+    ws = torch.empty(capi.moe_ffn_workspace_bytes(T, H, I, E, top_k), dtype=torch.uint8, device=dev)
+    y = torch.full((T * H,), float("nan"), dtype=torch.float32, device=dev)
+    capi.moe_ffn(d["x"], d["lg"], d["wg"], d["wu"], d["wd"], y, T, H, I, E, top_k, ws)
+    y_ffn = host(y).reshape(T, H)
+
+    # the same stages through their own entries
+    R = T * top_k
+    rw = torch.empty(R, dtype=torch.float32, device=dev)
+    ids = torch.empty(R, dtype=torch.int32, device=dev)
+    capi.moe_top_k(d["lg"], rw, ids, T, E, top_k)
+    xq = torch.empty(T * H // 128 * 144, dtype=torch.uint8, device=dev)
+    capi.quantize_q8_1(d["x"], xq, [H, T])
+    off = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    src = torch.empty(R, dtype=torch.int32, device=dev)
+    dst = torch.empty(R, dtype=torch.int32, device=dev)
+    xp = torch.empty(R * H // 128 * 144, dtype=torch.uint8, device=dev)
+    capi.moe_dispatch(ids, off, src, dst, T, top_k, H, E, xq=xq, xq_perm=xp)
+    gu = torch.empty(R * 2 * I, dtype=torch.float32, device=dev)
+    capi.moe_gate_up(d["wg"], d["wu"], xp, off, E, gu, H, I, R)
+    mq = torch.empty(R * I // 128 * 144, dtype=torch.uint8, device=dev)
+    capi.swiglu_quantize(gu, mq, R, I)
+    eo = torch.empty(R * H, dtype=torch.float32, device=dev)
+    capi.grouped_mat_mul(d["wd"], mq, off, eo, I, H, R)
+    y2 = torch.empty(T * H, dtype=torch.float32, device=dev)
+    capi.moe_combine(eo, dst, rw, y2, T, H, top_k)
+    assert np.array_equal(y_ffn, host(y2).reshape(T, H))
+
+    ref = _oracle_ffn(x, lg, wg, wu, wd, top_k)
+    np.testing.assert_allclose(y_ffn, ref, rtol=2e-3, atol=2e-3)
+
+
+def test_moe_ffn_rejects_small_workspace(dev):
+    import torch
+    T, H, I, E, k = 4, 128, 128, 4, 2
+    need = capi.moe_ffn_workspace_bytes(T, H, I, E, k)
+    ws = torch.empty(need - 256, dtype=torch.uint8, device=dev)
+    z = torch.zeros(1 << 20, dtype=torch.uint8, device=dev)
+    y = torch.empty(T * H, dtype=torch.float32, device=dev)
+    with pytest.raises(RuntimeError, match="workspace"):
+        capi.moe_ffn(z, z, z, z, z, y, T, H, I, E, k, ws)

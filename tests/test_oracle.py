@@ -350,3 +350,92 @@ def test_q4_0_packer_matches_oracle_and_bounds():
     nib = np.concatenate([a.reshape(33, 8, 18)[:, :, 2:] & 15, a.reshape(33, 8, 18)[:, :, 2:] >> 4], axis=2)
     bound = np.where(nib == 15, d[..., None], d[..., None] * 0.5) + slack
     assert np.all(err <= bound)
+
+
+# ---------------------------------------------------------------- MoE routing oracle pins
+def test_moe_top_k_selection_matches_stable_argsort():
+    """ids = experts sorted by descending logit, smaller id first on ties: the same
+    order as a stable argsort of -logits (a library routine)."""
+    rng = np.random.default_rng(7)
+    lg = rng.standard_normal((40, 8)).astype(np.float32)
+    lg[3] = 0.5  # all tied
+    lg[4, [1, 5, 6]] = 2.0  # partial tie at the top
+    for k in (1, 2, 3, 8):
+        ids, _ = oracle_np.moe_top_k(lg, k)
+        ref = np.argsort(-lg, axis=1, kind="stable")[:, :k]
+        assert np.array_equal(ids, ref)
+
+
+def test_moe_top_k_weights_are_softmax_of_selected():
+    rng = np.random.default_rng(8)
+    lg = (rng.standard_normal((50, 16)) * 3).astype(np.float32)
+    for k in (1, 2, 4, 7):
+        ids, w = oracle_np.moe_top_k(lg, k)
+        sel = np.take_along_axis(lg, ids, 1).astype(np.float64)
+        ex = np.exp(sel - sel.max(1, keepdims=True))
+        np.testing.assert_allclose(w, ex / ex.sum(1, keepdims=True), rtol=2e-6, atol=1e-7)
+    _, w1 = oracle_np.moe_top_k(lg, 1)
+    assert np.all(w1 == 1.0)
+
+
+def test_moe_top_k_sum_order_is_the_xor_butterfly():
+    """With 3 values in lanes 0..2 the butterfly computes (e0 + e2) + e1.  Witness:
+    e0 = 1, e1 = 2^-24, e2 = 1.5 * 2^-24 gives (e0+e2)+e1 = 1 + 2^-22, while
+    (e0+e1)+e2 and e0+(e1+e2) both give 1 + 2^-23."""
+    lanes = np.zeros(32, dtype=np.float32)
+    e0, e1, e2 = np.float32(1.0), np.float32(2.0 ** -24), np.float32(1.5 * 2.0 ** -24)
+    lanes[:3] = [e0, e1, e2]
+    b = oracle_np._xor_butterfly_sum32(lanes)
+    assert b == np.float32(1.0 + 2.0 ** -22)
+    assert (e0 + e1) + e2 == np.float32(1.0 + 2.0 ** -23) and e0 + (e1 + e2) == np.float32(1.0 + 2.0 ** -23)
+    for n in range(1, 33):
+        v = np.zeros(32, dtype=np.float32)
+        v[:n] = 1.0
+        assert oracle_np._xor_butterfly_sum32(v) == n
+
+
+def test_moe_dispatch_is_a_stable_sort():
+    rng = np.random.default_rng(9)
+    for T, k, E in ((64, 2, 8), (7, 1, 4), (100, 4, 16), (3, 3, 3)):
+        ids = rng.integers(0, E, size=(T, k)).astype(np.int32)
+        off, src, dst = oracle_np.moe_dispatch(ids, E)
+        flat = ids.reshape(-1)
+        assert np.array_equal(src, np.argsort(flat, kind="stable"))
+        assert np.array_equal(off, np.searchsorted(np.sort(flat), np.arange(E + 1), side="left"))
+        assert np.array_equal(dst[src], np.arange(T * k))
+
+
+def test_gather_q8_1_bruteforce():
+    rng = np.random.default_rng(10)
+    T, k, K = 5, 2, 256
+    xq = rng.integers(0, 256, size=T * K // 128 * 144).astype(np.uint8)
+    src = rng.permutation(T * k).astype(np.int32)
+    got = oracle_np.gather_q8_1(xq, src, T, k, K).reshape(K // 128, T * k, 144)
+    blocks = xq.reshape(K // 128, T, 144)
+    for s in range(K // 128):
+        for p in range(T * k):
+            assert np.array_equal(got[s, p], blocks[s, src[p] // k])
+
+
+def test_swiglu_closed_forms():
+    g = np.array([0.0, 1.0, -1.0, 30.0, -30.0, 4.5], dtype=np.float32)
+    u = np.array([3.0, 2.0, 2.0, 1.0, 1.0, -0.5], dtype=np.float32)
+    got = oracle_np.swiglu(g, u).astype(np.float64)
+    exact = g.astype(np.float64) / (1.0 + np.exp(-g.astype(np.float64))) * u
+    np.testing.assert_allclose(got, exact, rtol=1e-6, atol=1e-30)
+    assert got[0] == 0.0 and got[3] == 30.0  # silu(0) = 0, silu(30) = 30 in fp32
+
+
+def test_moe_combine_closed_forms():
+    rng = np.random.default_rng(11)
+    T, k, H = 6, 3, 16
+    eo = rng.standard_normal((T * k, H)).astype(np.float32)
+    dst = rng.permutation(T * k).astype(np.int32)
+    w = rng.random(T * k).astype(np.float32)
+    y = oracle_np.moe_combine(eo, dst, w, k)
+    ref = np.stack([sum(np.float64(w[t * k + j]) * eo[dst[t * k + j]].astype(np.float64) for j in range(k))
+                    for t in range(T)])
+    np.testing.assert_allclose(y, ref, rtol=1e-6, atol=1e-7)
+    # top_k = 1 and weight 1: the inverse permutation, exactly
+    y1 = oracle_np.moe_combine(eo, dst, np.ones(T * k, np.float32), 1)
+    assert np.array_equal(y1, eo[dst])
