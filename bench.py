@@ -184,6 +184,41 @@ def time_moe(dev, steps, warmup):
             "kernel_hbm_frac": alg_bytes / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
+def time_moe_ffn(dev, steps, warmup):
+    """The whole Q4_0 MoE FFN of the same layer shape (8 experts, top-2, 512 tokens,
+    H=4096, I=14336): quantize, top-k, dispatch, gate|up, SwiGLU+quantize, down,
+    combine -- eight launches per step, captured in one graph."""
+    import torch
+    from jjjetson_ops_amd import capi
+
+    E, T, topk, H, I = 8, 512, 2, 4096, 14336
+    g = torch.Generator(device="cpu").manual_seed(4)
+    logits = torch.randn(T, E, generator=g).to(dev)
+    wg = torch.cat([make_weights(I, H, 60 + e, dev, 1)[0] for e in range(E)])
+    wu = torch.cat([make_weights(I, H, 70 + e, dev, 1)[0] for e in range(E)])
+    wd = torch.cat([make_weights(H, I, 80 + e, dev, 1)[0] for e in range(E)])
+    x = make_x(T, H, 46, dev, True)
+    y = torch.empty(T * H, dtype=torch.float32, device=dev)
+    ws = torch.empty(capi.moe_ffn_workspace_bytes(T, H, I, E, topk), dtype=torch.uint8, device=dev)
+
+    def step(i):
+        capi.moe_ffn(x, logits, wg, wu, wd, y, T, H, I, E, topk, ws)
+
+    for i in range(warmup):
+        step(i)
+    gr = _graph(step, steps)
+    gr.replay()
+    avg = _time_graph(gr) / steps
+    R = T * topk
+    ops = 2.0 * R * 3 * I * H
+    wbytes = 3 * E * I * (H // 32) * 18  # 792 MB: every step streams past the MALL
+    del gr
+    torch.cuda.empty_cache()
+    return {"name": "moe_ffn_q4_0_e8_top2_t512_h4096_i14336", "routes": R, "H": H, "I": I,
+            "us_per_step": avg * 1e3, "TOPS": ops / (avg * 1e-3) / 1e12,
+            "mfma_frac": ops / (avg * 1e-3) / 1e12 / INT8_PEAK_TOPS,
+            "weight_GBps": wbytes / (avg * 1e-3) / 1e9, "launches_per_step": 8}
+
 def _traffic(workload):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary (FETCH_SIZE and
     WRITE_SIZE, each scaled by the same counters' reading for a torch copy kernel of
@@ -300,6 +335,8 @@ def main():
     if args.only:
         if args.only == "moe_grouped_e8_top2_t512":
             res = time_moe(dev, max(10, args.steps // 10), 3)
+        elif args.only == "moe_ffn":
+            res = time_moe_ffn(dev, max(5, args.steps // 20), 2)
         else:
             sel = [p for p in plan if p[0] == args.only]
             if not sel:
@@ -330,6 +367,8 @@ def main():
             configs.append(time_linear(name, M, K, N, seed, dev, st, max(3, args.warmup // 4)))
         log("bench: moe grouped")
         configs.append(time_moe(dev, max(10, args.steps // 10), 3))
+        log("bench: moe ffn")
+        configs.append(time_moe_ffn(dev, max(5, args.steps // 20), 2))
 
     cpu = None
     if not args.no_cpu:
