@@ -36,6 +36,8 @@
 //     stage's MFMA/epilogue work (register double buffering).
 #include <hip/hip_fp16.h>
 
+#include <type_traits>
+
 #include "q4q8_common.hpp"
 
 namespace jjo {
@@ -104,7 +106,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = wave >> 1;  // row half of the workgroup tile
     const int wm = wave & 1;   // token half
     const int l32 = lane & 31;
@@ -242,10 +244,15 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     i32x16 bias;
 #pragma unroll
     for (int v = 0; v < 16; ++v) bias[v] = (int32_t)kBiasBits;
+    // Opaque to the optimizer: the 16 bias registers stay resident instead of being
+    // re-materialized (16 v_mov) before every MFMA whose result reuses them.
+    asm volatile("" : "+v"(bias));
 
     // Columns past m_end hold stale LDS bytes: their scales are forced to zero.
     const bool col_ok[2] = {m0 + wm * 64 + l32 < m_end, m0 + wm * 64 + 32 + l32 < m_end};
-    const bool ct_live[2] = {m0 + wm * 64 < m_end, m0 + wm * 64 + 32 < m_end};  // wave-uniform
+    // 32-token sub-tiles of this wave that hold valid tokens (grouped tails have 0 or
+    // 1): a compile-time parameter of the stage loop below, chosen once per wave.
+    const int n_live = (m0 + wm * 64 < m_end) + (m0 + wm * 64 + 32 < m_end);
 
     // Pipeline, one barrier per stage: while stage c is computed from buffers c&1,
     // the loads of stage c+1 are in flight; stage c+1's weights are unpacked into the
@@ -260,108 +267,116 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
         load_w(1);
     }
 
-    for (int c = 0; c < n_stages; ++c) {
-        uint8_t *wq = smem + kOffW + (c & 1) * kWBufBytes;
-        const _Float16 *wd_epi = reinterpret_cast<const _Float16 *>(wq + kOffWdEpi);
-        const _Float16 *wd_row = reinterpret_cast<const _Float16 *>(wq + kOffWdRow);
-        const uint8_t *xs = smem + (c & 1) * kXsBytes;
+    auto stage_loop = [&](auto live_tag) {
+        constexpr int LIVE = decltype(live_tag)::value;
+        for (int c = 0; c < n_stages; ++c) {
+            uint8_t *wq = smem + kOffW + (c & 1) * kWBufBytes;
+            const _Float16 *wd_epi = reinterpret_cast<const _Float16 *>(wq + kOffWdEpi);
+            const _Float16 *wd_row = reinterpret_cast<const _Float16 *>(wq + kOffWdRow);
+            const uint8_t *xs = smem + (c & 1) * kXsBytes;
 
-        // Activation headers (d, s) of this lane's two columns.
-        uint32_t hdr[2][4];
-#pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-            const int col = wm * 64 + ct * 32 + l32;
-            const u32x4 h = *reinterpret_cast<const u32x4 *>(xs + col * kQ8BlockBytes);
-            hdr[ct][0] = col_ok[ct] ? h.x : 0u; hdr[ct][1] = col_ok[ct] ? h.y : 0u;
-            hdr[ct][2] = col_ok[ct] ? h.z : 0u; hdr[ct][3] = col_ok[ct] ? h.w : 0u;
-        }
-
-        // Token sub-tiles past the last valid token (grouped tails) skip the math:
-        // wave-uniform branches.
-        if (!ct_live[0]) goto stage_done;
-#pragma unroll
-        for (int b = 0; b < KB; ++b) {
-            i32x4 bop[2], aop[2];
-#pragma unroll
+            // Activation headers (d, s) of this lane's two columns.
+            uint32_t hdr[2][4];
+    #pragma unroll
             for (int ct = 0; ct < 2; ++ct) {
                 const int col = wm * 64 + ct * 32 + l32;
-                bop[ct] = *reinterpret_cast<const i32x4 *>(xs + col * kQ8BlockBytes + 16 + 32 * b + 16 * hh);
+                const u32x4 h = *reinterpret_cast<const u32x4 *>(xs + col * kQ8BlockBytes);
+                hdr[ct][0] = col_ok[ct] ? h.x : 0u; hdr[ct][1] = col_ok[ct] ? h.y : 0u;
+                hdr[ct][2] = col_ok[ct] ? h.z : 0u; hdr[ct][3] = col_ok[ct] ? h.w : 0u;
             }
-#pragma unroll
-            for (int rt = 0; rt < 2; ++rt) {
-                const int row = wn * 64 + rt * 32 + l32;
-                aop[rt] = *reinterpret_cast<const i32x4 *>(wq + row * kWqStride + b * 32 + 16 * hh);
+
+            if constexpr (LIVE > 0) {
+    #pragma unroll
+            for (int b = 0; b < KB; ++b) {
+                i32x4 bop[2], aop[2];
+    #pragma unroll
+                for (int ct = 0; ct < 2; ++ct) {
+                    const int col = wm * 64 + ct * 32 + l32;
+                    bop[ct] = *reinterpret_cast<const i32x4 *>(xs + col * kQ8BlockBytes + 16 + 32 * b + 16 * hh);
+                }
+    #pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    const int row = wn * 64 + rt * 32 + l32;
+                    aop[rt] = *reinterpret_cast<const i32x4 *>(wq + row * kWqStride + b * 32 + 16 * hh);
+                }
+                float dx8[2], nb8[2];
+    #pragma unroll
+                for (int ct = 0; ct < 2; ++ct) {
+                    const float dx = __half2float(__ushort_as_half((unsigned short)(hdr[ct][b] & 0xffffu)));
+                    dx8[ct] = dx * 0.125f;
+                    nb8[ct] = -kBias * dx8[ct];
+                }
+                uint32_t wv[2][8];
+    #pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    const int rbase = (wn * 2 + rt) * 32 + hh * 16;
+                    const u32x4 w0 = *reinterpret_cast<const u32x4 *>(wd_epi + b * BN + rbase);
+                    const u32x4 w1 = *reinterpret_cast<const u32x4 *>(wd_epi + b * BN + rbase + 8);
+                    wv[rt][0] = w0.x; wv[rt][1] = w0.y; wv[rt][2] = w0.z; wv[rt][3] = w0.w;
+                    wv[rt][4] = w1.x; wv[rt][5] = w1.y; wv[rt][6] = w1.z; wv[rt][7] = w1.w;
+                }
+                // Two result tiles in flight: the MFMA of the next tile overlaps the
+                // VALU epilogue of the previous one.
+                if constexpr (LIVE == 2) {
+                    i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[0], bop[0], bias, 0, 0, 0);
+                    i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[0], bop[1], bias, 0, 0, 0);
+                    epilogue(acc[0][0], d0, wv[0], dx8[0], nb8[0]);
+                    d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[1], bop[0], bias, 0, 0, 0);
+                    epilogue(acc[0][1], d1, wv[0], dx8[1], nb8[1]);
+                    d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[1], bop[1], bias, 0, 0, 0);
+                    epilogue(acc[1][0], d0, wv[1], dx8[0], nb8[0]);
+                    epilogue(acc[1][1], d1, wv[1], dx8[1], nb8[1]);
+                } else {
+                    const i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[0], bop[0], bias, 0, 0, 0);
+                    const i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[1], bop[0], bias, 0, 0, 0);
+                    epilogue(acc[0][0], d0, wv[0], dx8[0], nb8[0]);
+                    epilogue(acc[1][0], d1, wv[1], dx8[0], nb8[0]);
+                }
             }
-            float dx8[2], nb8[2];
-#pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
-                const float dx = __half2float(__ushort_as_half((unsigned short)(hdr[ct][b] & 0xffffu)));
-                dx8[ct] = dx * 0.125f;
-                nb8[ct] = -kBias * dx8[ct];
+
+            // sum_b d_w * (-s_x) over this stage's 4 blocks on the f16 MFMA (K = 8:
+            // the lanes of the upper K half contribute zeros).
+            {
+                f16x4 aop[2], bop[2];
+    #pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    const int row = wn * 64 + rt * 32 + l32;
+                    aop[rt] = *reinterpret_cast<const f16x4 *>(wd_row + row * KB);
+                }
+    #pragma unroll
+                for (int ct = 0; ct < 2; ++ct) {
+                    const uint32_t *h = hdr[ct];
+                    uint32_t lo = ((h[0] >> 16) | (h[1] & 0xffff0000u)) ^ 0x80008000u;
+                    uint32_t hi = ((h[2] >> 16) | (h[3] & 0xffff0000u)) ^ 0x80008000u;
+                    if (hh) { lo = 0u; hi = 0u; }
+                    const u32x2 pk = {lo, hi};
+                    bop[ct] = __builtin_bit_cast(f16x4, pk);
+                }
+    #pragma unroll
+                for (int rt = 0; rt < 2; ++rt)
+    #pragma unroll
+                    for (int ct = 0; ct < 2; ++ct)
+                        acc[rt][ct] = __builtin_amdgcn_mfma_f32_32x32x8f16(aop[rt], bop[ct], acc[rt][ct], 0, 0, 0);
             }
-            uint32_t wv[2][8];
-#pragma unroll
-            for (int rt = 0; rt < 2; ++rt) {
-                const int rbase = (wn * 2 + rt) * 32 + hh * 16;
-                const u32x4 w0 = *reinterpret_cast<const u32x4 *>(wd_epi + b * BN + rbase);
-                const u32x4 w1 = *reinterpret_cast<const u32x4 *>(wd_epi + b * BN + rbase + 8);
-                wv[rt][0] = w0.x; wv[rt][1] = w0.y; wv[rt][2] = w0.z; wv[rt][3] = w0.w;
-                wv[rt][4] = w1.x; wv[rt][5] = w1.y; wv[rt][6] = w1.z; wv[rt][7] = w1.w;
-            }
-            // Two result tiles in flight: the MFMA of the next tile overlaps the
-            // VALU epilogue of the previous one.
-            if (ct_live[1]) {
-                i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[0], bop[0], bias, 0, 0, 0);
-                i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[0], bop[1], bias, 0, 0, 0);
-                epilogue(acc[0][0], d0, wv[0], dx8[0], nb8[0]);
-                d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[1], bop[0], bias, 0, 0, 0);
-                epilogue(acc[0][1], d1, wv[0], dx8[1], nb8[1]);
-                d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[1], bop[1], bias, 0, 0, 0);
-                epilogue(acc[1][0], d0, wv[1], dx8[0], nb8[0]);
-                epilogue(acc[1][1], d1, wv[1], dx8[1], nb8[1]);
-            } else {
-                const i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[0], bop[0], bias, 0, 0, 0);
-                const i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[1], bop[0], bias, 0, 0, 0);
-                epilogue(acc[0][0], d0, wv[0], dx8[0], nb8[0]);
-                epilogue(acc[1][0], d1, wv[1], dx8[0], nb8[0]);
+            }  // LIVE > 0
+
+            if (c + 1 < n_stages) {
+                store_w((c + 1) & 1);  // waits for W(c+1) and X(c+1), issued a compute phase ago
+                __syncthreads();
+                if (c + 2 < n_stages) {
+                    load_x(c + 2);
+                    load_w(c + 2);
+                }
             }
         }
 
-        // sum_b d_w * (-s_x) over this stage's 4 blocks on the f16 MFMA (K = 8:
-        // the lanes of the upper K half contribute zeros).
-        {
-            f16x4 aop[2], bop[2];
-#pragma unroll
-            for (int rt = 0; rt < 2; ++rt) {
-                const int row = wn * 64 + rt * 32 + l32;
-                aop[rt] = *reinterpret_cast<const f16x4 *>(wd_row + row * KB);
-            }
-#pragma unroll
-            for (int ct = 0; ct < 2; ++ct) {
-                const uint32_t *h = hdr[ct];
-                uint32_t lo = ((h[0] >> 16) | (h[1] & 0xffff0000u)) ^ 0x80008000u;
-                uint32_t hi = ((h[2] >> 16) | (h[3] & 0xffff0000u)) ^ 0x80008000u;
-                if (hh) { lo = 0u; hi = 0u; }
-                const u32x2 pk = {lo, hi};
-                bop[ct] = __builtin_bit_cast(f16x4, pk);
-            }
-#pragma unroll
-            for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-                for (int ct = 0; ct < 2; ++ct)
-                    acc[rt][ct] = __builtin_amdgcn_mfma_f32_32x32x8f16(aop[rt], bop[ct], acc[rt][ct], 0, 0, 0);
-        }
-
-    stage_done:
-        if (c + 1 < n_stages) {
-            store_w((c + 1) & 1);  // waits for W(c+1) and X(c+1), issued a compute phase ago
-            __syncthreads();
-            if (c + 2 < n_stages) {
-                load_x(c + 2);
-                load_w(c + 2);
-            }
-        }
-    }
+    };
+    if (n_live == 2)
+        stage_loop(std::integral_constant<int, 2>{});
+    else if (n_live == 1)
+        stage_loop(std::integral_constant<int, 1>{});
+    else
+        stage_loop(std::integral_constant<int, 0>{});
 
     // ---- store: y[m][n] = 8 * acc ----
 #pragma unroll
