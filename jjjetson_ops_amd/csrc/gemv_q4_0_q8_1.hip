@@ -400,10 +400,16 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
 #ifndef JJO_GEMV1_U
 #define JJO_GEMV1_U 2
 #endif
+#ifndef JJO_GEMVM_RG1
+#define JJO_GEMVM_RG1 4
+#endif
+#ifndef JJO_GEMV4_U
+#define JJO_GEMV4_U 4
+#endif
 template <int M, int JS>
 constexpr int rg_for() {
     if (M == 1) return JS == 1 ? JJO_GEMV1_RG1 : JS == 2 ? 4 : JS == 3 ? 4 : 2;
-    return JS == 1 ? 4 : JS == 2 ? 2 : 1;
+    return JS == 1 ? JJO_GEMVM_RG1 : JS == 2 ? 2 : 1;
 }
 
 template <int M, int U, int JS, bool FUSED, int EARLY>
@@ -456,9 +462,9 @@ hipError_t launch_gemv_dot4(const void *w, const void *xq, float *y, int K, int 
                             hipStream_t stream) {
     switch (M) {
         case 1: return launch_m<1, JJO_GEMV1_U, false>(w, xq, nullptr, y, K, N, stream);
-        case 2: return launch_m<2, 4, false>(w, xq, nullptr, y, K, N, stream);
+        case 2: return launch_m<2, 2, false>(w, xq, nullptr, y, K, N, stream);
         case 3: return launch_m<3, 4, false>(w, xq, nullptr, y, K, N, stream);
-        case 4: return launch_m<4, 4, false>(w, xq, nullptr, y, K, N, stream);
+        case 4: return launch_m<4, JJO_GEMV4_U, false>(w, xq, nullptr, y, K, N, stream);
         case 5: return launch_m<5, 2, false>(w, xq, nullptr, y, K, N, stream);
         case 6: return launch_m<6, 2, false>(w, xq, nullptr, y, K, N, stream);
         case 7: return launch_m<7, 2, false>(w, xq, nullptr, y, K, N, stream);
