@@ -122,7 +122,9 @@ int validate_mm(const void *w, const void *xq, const void *y, int K, int N, int 
 int run_mm(const void *w, const void *xq, float *y, int K, int N, int M, int algo, hipStream_t s) {
     if (algo == JJO_ALGO_AUTO) {
         const bool gemv_ok = M <= kGemvMaxBatch && K <= kGemvMaxK && (int64_t)M * (K / 64) * 80 <= 150 * 1024;
-        if (gemv_ok && M <= kGemvPreferredBatch)
+        // The GEMV wins up to batch 4 on rows of one K-slice (K <= 4096); with more
+        // slices its per-token cost grows and the skinny kernel wins from batch 3.
+        if (gemv_ok && M <= (K <= 4096 ? kGemvPreferredBatch : 2))
             algo = JJO_ALGO_GEMV;
         else if (gemm_skinny_supported(w, xq, K, M))
             algo = JJO_ALGO_SKINNY;

@@ -50,7 +50,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int kWaves = 4;  // K-slices per workgroup
 constexpr int kStageBlocks = 8;
 constexpr int kStageRowBytes = kStageBlocks * kQ4BlockBytes;  // 144
 constexpr uint32_t kBiasBits = 0x4B400000u;
@@ -84,27 +83,27 @@ struct Geo {
     static constexpr int kScBytes = kStageBlocks * 2 * 16 * CT * 4;   // dx8, nb8 per block/token
 };
 
-template <int RT, int CT, int P>
+template <int RT, int CT, int P, int KW>
 struct Lds {
     static constexpr int kWaveBytes = P * Geo<RT, CT>::kStageBytes + Geo<RT, CT>::kScBytes;
-    static constexpr int kBytes = kWaves * kWaveBytes;
-    static constexpr int kRedBytes = kWaves * RT * CT * 64 * 16;
+    static constexpr int kBytes = KW * kWaveBytes;
+    static constexpr int kRedBytes = KW * RT * CT * 64 * 16;
     static_assert(kRedBytes <= kBytes, "reduction area must fit the rings");
 };
 
 #ifdef JJO_SKINNY_TRACE
-__device__ unsigned long long g_skinny_trace[4096 * 4][16];
-#define TR(i) if (lane == 0 && blockIdx.x < 4096) g_skinny_trace[blockIdx.x * 4 + wave][i] = __builtin_amdgcn_s_memrealtime()
+__device__ unsigned long long g_skinny_trace[4096 * 8][16];
+#define TR(i) if (lane == 0 && blockIdx.x * KW + wave < 4096 * 8) g_skinny_trace[blockIdx.x * KW + wave][i] = __builtin_amdgcn_s_memrealtime()
 #else
 #define TR(i)
 #endif
 
-template <int RT, int CT, int P>
-__global__ __launch_bounds__(64 * kWaves) void gemm_skinny_kernel(const uint8_t *__restrict__ w,
+template <int RT, int CT, int P, int KW>
+__global__ __launch_bounds__(64 * KW) void gemm_skinny_kernel(const uint8_t *__restrict__ w,
                                                                   const uint8_t *__restrict__ xq,
                                                                   float *__restrict__ y, int K, int N, int M) {
     using G = Geo<RT, CT>;
-    using L = Lds<RT, CT, P>;
+    using L = Lds<RT, CT, P, KW>;
     __shared__ __align__(16) uint8_t smem[L::kBytes];
 
     const int lane = threadIdx.x & 63;
@@ -119,7 +118,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_skinny_kernel(const uint8_t 
     // Stages of this wave: wave, wave + 4, wave + 8, ...  The 4 waves of the
     // workgroup read adjacent 144-byte pieces of the same rows at the same time,
     // 576 contiguous bytes per row, which keeps HBM pages and L2 lines shared.
-    const int n_my = (n_stages - wave + kWaves - 1) / kWaves;
+    const int n_my = (n_stages - wave + KW - 1) / KW;
 
     uint8_t *ring = smem + wave * L::kWaveBytes;
     float *sc = reinterpret_cast<float *>(ring + P * G::kStageBytes);
@@ -143,7 +142,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_skinny_kernel(const uint8_t 
 
     auto issue = [&](int s) {  // stage s of this wave's slice into slot s % P
         uint8_t *st = ring + (s % P) * G::kStageBytes;
-        const int gs = wave + kWaves * s;
+        const int gs = wave + KW * s;
         const uint8_t *ws = w_base + (size_t)gs * kStageRowBytes;
 #pragma unroll
         for (int i = 0; i < G::kWInstr; ++i) {
@@ -296,7 +295,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_skinny_kernel(const uint8_t 
             for (int ct = 0; ct < CT; ++ct) {
                 f32x4 sum = red[((0 * RT + rt) * CT + ct) * 64 + lane];
 #pragma unroll
-                for (int k = 1; k < kWaves; ++k) sum = sum + red[((k * RT + rt) * CT + ct) * 64 + lane];
+                for (int k = 1; k < KW; ++k) sum = sum + red[((k * RT + rt) * CT + ct) * 64 + lane];
                 const int n = n0 + 16 * rt + l16;
                 if (n < N) {
 #pragma unroll
@@ -310,10 +309,10 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_skinny_kernel(const uint8_t 
     TR(15);
 }
 
-template <int RT, int CT, int P>
+template <int RT, int CT, int P, int KW>
 hipError_t launch_rcp(const void *w, const void *xq, float *y, int K, int N, int M, hipStream_t stream) {
     const int blocks = (N + 16 * RT - 1) / (16 * RT);
-    hipLaunchKernelGGL((gemm_skinny_kernel<RT, CT, P>), dim3(blocks), dim3(64 * kWaves), 0, stream,
+    hipLaunchKernelGGL((gemm_skinny_kernel<RT, CT, P, KW>), dim3(blocks), dim3(64 * KW), 0, stream,
                        (const uint8_t *)w, (const uint8_t *)xq, y, K, N, M);
     return hipGetLastError();
 }
@@ -333,8 +332,14 @@ bool gemm_skinny_supported(const void *w, const void *xq, int K, int M) {
 
 hipError_t launch_gemm_skinny(const void *w, const void *xq, float *y, int K, int N, int M, hipStream_t stream) {
     if (!gemm_skinny_supported(w, xq, K, M)) return hipErrorInvalidValue;
-    if (M <= 16) return launch_rcp<JJO_SKINNY_RT, 1, JJO_SKINNY_P>(w, xq, y, K, N, M, stream);
-    return launch_rcp<JJO_SKINNY_RT, 2, JJO_SKINNY_P>(w, xq, y, K, N, M, stream);
+    if (M <= 16) {
+        // 32-row workgroups of 4 K-slice waves while that fills the chip; for short
+        // matrices (N < 8192) 16-row workgroups of 8 K-slice waves (twice the
+        // workgroups, each CU holding one).
+        if ((N + 31) / 32 >= 256) return launch_rcp<JJO_SKINNY_RT, 1, JJO_SKINNY_P, 4>(w, xq, y, K, N, M, stream);
+        return launch_rcp<1, 1, JJO_SKINNY_P, 8>(w, xq, y, K, N, M, stream);
+    }
+    return launch_rcp<JJO_SKINNY_RT, 2, JJO_SKINNY_P, 4>(w, xq, y, K, N, M, stream);
 }
 
 #ifdef JJO_SKINNY_TRACE
