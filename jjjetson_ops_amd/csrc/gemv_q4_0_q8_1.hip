@@ -400,6 +400,9 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
 #ifndef JJO_GEMV1_U
 #define JJO_GEMV1_U 2
 #endif
+#ifndef JJO_GEMV1_RG3
+#define JJO_GEMV1_RG3 4
+#endif
 #ifndef JJO_GEMVM_RG1
 #define JJO_GEMVM_RG1 4
 #endif
@@ -408,7 +411,7 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
 #endif
 template <int M, int JS>
 constexpr int rg_for() {
-    if (M == 1) return JS == 1 ? JJO_GEMV1_RG1 : JS == 2 ? 4 : JS == 3 ? 4 : 2;
+    if (M == 1) return JS == 1 ? JJO_GEMV1_RG1 : JS == 2 ? 4 : JS == 3 ? JJO_GEMV1_RG3 : 2;
     return JS == 1 ? JJO_GEMVM_RG1 : JS == 2 ? 2 : 1;
 }
 
