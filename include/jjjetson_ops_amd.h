@@ -249,6 +249,70 @@ int moe_q4_0_ffn_forward_device(void *stream, const float *x, const float *logit
                                 int intermediate_size, int num_experts, int top_k, void *workspace,
                                 int64_t workspace_bytes);
 
+/* ------------------------------------------------------------------ Q4_0 weights on disk
+ * The reference's loader holds F32 tensors only (WeightDtype, src/model/weight_loader.h:12-14;
+ * HostTensor, :17-23).  These entries add Q4_0: a tensor of logical shape
+ * [rows, cols] (rows = out_features, cols = in_features, as the engine's weights,
+ * src/cuda/linear.cu:19) stored in a .safetensors file as dtype "U8", shape
+ * [rows, cols/32, 18] (block_q4_0, row-major: the layout every kernel above reads),
+ * marked by the header metadata entry "q4_0:<name>": "Q4_0".
+ * Quantization rule (ggml's Q4_0, which the reference's MMQ consumes): per 32 values
+ * mx = the value of largest magnitude (first on ties), d = mx / -8 stored fp16,
+ * id = d != 0 ? 1/d : 0, nib = clamp((int)(v*id + 8.5), 0, 15).
+ */
+#define JJO_WEIGHT_DTYPE_F32 0  /* WEIGHT_DTYPE_F32 (weight_loader.h:13) */
+#define JJO_WEIGHT_DTYPE_Q4_0 1 /* new: block_q4_0 bytes */
+
+typedef struct jjo_host_tensor {
+    char *name;
+    void *data;      /* F32: float[numel]; Q4_0: rows*(cols/32) blocks of 18 bytes */
+    int64_t *dims;   /* logical shape; Q4_0 tensors are [rows, cols] */
+    int ndim;
+    int dtype;       /* JJO_WEIGHT_DTYPE_* */
+    int64_t nbytes;  /* bytes at data */
+} jjo_host_tensor;
+
+/* Bytes of a [rows, cols] Q4_0 matrix; -1 unless rows > 0 and cols is a positive multiple of 32. */
+int64_t q4_0_bytes(int64_t rows, int64_t cols);
+
+/*
+ * Host fp32 [rows][cols] -> Q4_0 (num_threads <= 0: one per hardware thread).
+ * No counterpart in the reference (it ships no Q4_0 quantizer); the repacker's kernel.
+ */
+int quantize_q4_0_host(const float *w, void *out, int64_t rows, int64_t cols, int num_threads);
+
+/*
+ * The same quantizer on device pointers (one launch, asynchronous on `stream`,
+ * bit-identical to quantize_q4_0_host).  w 16-byte aligned.
+ */
+int quantize_q4_0_device(void *stream, const float *d_w, void *d_out, int64_t rows, int64_t cols);
+
+/*
+ * Reads every tensor of a .safetensors file: F32 tensors and Q4_0 tensors (marked
+ * as above); any other dtype is an error.  Replaces safetensors_read_file
+ * (src/model/safetensors_reader.h:10, safetensors_reader.cpp:369-494).  The caller
+ * frees the array with jjo_host_tensors_free (weight_load_result_destroy,
+ * weight_loader.h:34).  Returns 0 or a JJO_ERR_* code (nothing allocated on error).
+ */
+int safetensors_read_file_q4_0(const char *path, jjo_host_tensor **out_tensors, int *out_num_tensors);
+void jjo_host_tensors_free(jjo_host_tensor *tensors, int num_tensors);
+/* weight_load_result_find (weight_loader.h:36): the tensor named `name`, or NULL. */
+const jjo_host_tensor *jjo_host_tensors_find(const jjo_host_tensor *tensors, int num_tensors, const char *name);
+
+/*
+ * Writes tensors (F32 or Q4_0, in the given order) as a standard .safetensors file.
+ * No counterpart in the reference (its loader only reads).
+ */
+int safetensors_write_file_q4_0(const char *path, const jjo_host_tensor *tensors, int num_tensors);
+
+/*
+ * Offline repacker: copies in_path to out_path with the named 2-D F32 tensors
+ * (cols % 32 == 0) quantized to Q4_0, or every such tensor when num_names < 0.
+ * Streams one tensor at a time.  No counterpart in the reference.
+ */
+int safetensors_quantize_q4_0(const char *in_path, const char *out_path, const char *const *names, int num_names,
+                              int num_threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -52,7 +52,30 @@ EXPORTED_SYMBOLS = (
     "moe_combine_device",
     "moe_q4_0_ffn_workspace_bytes",
     "moe_q4_0_ffn_forward_device",
+    "q4_0_bytes",
+    "quantize_q4_0_host",
+    "quantize_q4_0_device",
+    "safetensors_read_file_q4_0",
+    "jjo_host_tensors_free",
+    "jjo_host_tensors_find",
+    "safetensors_write_file_q4_0",
+    "safetensors_quantize_q4_0",
 )
+
+WEIGHT_DTYPE_F32 = 0
+WEIGHT_DTYPE_Q4_0 = 1
+
+
+class HostTensor(ctypes.Structure):
+    """jjo_host_tensor (include/jjjetson_ops_amd.h)."""
+    _fields_ = [
+        ("name", ctypes.c_char_p),
+        ("data", ctypes.c_void_p),
+        ("dims", ctypes.POINTER(ctypes.c_int64)),
+        ("ndim", ctypes.c_int),
+        ("dtype", ctypes.c_int),
+        ("nbytes", ctypes.c_int64),
+    ]
 
 
 class JJOError(RuntimeError):
@@ -119,6 +142,24 @@ def lib() -> ctypes.CDLL:
         L.moe_q4_0_ffn_workspace_bytes.argtypes = [i32, i32, i32, i32, i32]
         L.moe_q4_0_ffn_forward_device.restype = i32
         L.moe_q4_0_ffn_forward_device.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp, i64]
+        L.q4_0_bytes.restype = i64
+        L.q4_0_bytes.argtypes = [i64, i64]
+        L.quantize_q4_0_host.restype = i32
+        L.quantize_q4_0_host.argtypes = [vp, vp, i64, i64, i32]
+        L.quantize_q4_0_device.restype = i32
+        L.quantize_q4_0_device.argtypes = [vp, vp, vp, i64, i64]
+        ht_p = ctypes.POINTER(HostTensor)
+        L.safetensors_read_file_q4_0.restype = i32
+        L.safetensors_read_file_q4_0.argtypes = [ctypes.c_char_p, ctypes.POINTER(ht_p), ctypes.POINTER(i32)]
+        L.jjo_host_tensors_free.restype = None
+        L.jjo_host_tensors_free.argtypes = [ht_p, i32]
+        L.jjo_host_tensors_find.restype = ht_p
+        L.jjo_host_tensors_find.argtypes = [ht_p, i32, ctypes.c_char_p]
+        L.safetensors_write_file_q4_0.restype = i32
+        L.safetensors_write_file_q4_0.argtypes = [ctypes.c_char_p, ht_p, i32]
+        L.safetensors_quantize_q4_0.restype = i32
+        L.safetensors_quantize_q4_0.argtypes = [ctypes.c_char_p, ctypes.c_char_p,
+                                                ctypes.POINTER(ctypes.c_char_p), i32, i32]
         _lib = L
     return _lib
 

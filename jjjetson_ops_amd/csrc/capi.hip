@@ -380,6 +380,24 @@ int mat_mul_q4_0_q8_1(const void *weight_q4_0, const float *input, uint8_t *quan
     return rc;
 }
 
+// ---------------------------------------------------------------- Q4_0 weights
+int quantize_q4_0_device(void *stream, const float *d_w, void *d_out, int64_t rows, int64_t cols) {
+    clear_error();
+    if (d_w == nullptr || d_out == nullptr) return set_error(JJO_ERR_INVALID_ARG, "null pointer argument");
+    if (q4_0_bytes(rows, cols) < 0)
+        return set_error(JJO_ERR_INVALID_ARG, "rows (%lld) and cols (%lld) must be positive, cols a multiple of 32",
+                         (long long)rows, (long long)cols);
+    if (!aligned(d_w, 16)) return set_error(JJO_ERR_INVALID_ARG, "weight pointer must be 16-byte aligned");
+    if (rows * (cols / JJO_QK4_0) > (int64_t)0x7fffffff * 64)
+        return set_error(JJO_ERR_INVALID_ARG, "matrix too large for one launch (%lld blocks)",
+                         (long long)(rows * (cols / JJO_QK4_0)));
+    int rc = require_gfx950();
+    if (rc != JJO_OK) return rc;
+    hipError_t e = launch_quantize_q4_0(d_w, d_out, rows * (cols / JJO_QK4_0), (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "quantize_q4_0 launch");
+    return JJO_OK;
+}
+
 // ---------------------------------------------------------------- engine linear
 int64_t linear_q4_0_workspace_bytes(int in_features, int num_tokens) {
     if (in_features <= 0 || num_tokens <= 0 || in_features % kQSuper != 0) return -1;

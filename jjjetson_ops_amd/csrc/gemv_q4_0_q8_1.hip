@@ -178,8 +178,11 @@ __device__ __forceinline__ void issue_f32(ItemF32 &it, const float *__restrict__
 // roundf (ties away from zero) for |v| < 2^23 in three ops: adding 0.5 - 2^-25
 // with v's sign and truncating gives the same integer as roundf for every such
 // float (checked exhaustively over all 2^30 non-negative floats below 2^23 in
-// the test suite; the sign makes it symmetric).
+// the test suite; the sign makes it symmetric).  `v` must be the rounded fp32
+// product: contraction of the caller's multiply into this add (an fma) would skip
+// that rounding and move products just below a .5 tie that round up onto it.
 __device__ __forceinline__ int32_t round_away(float v) {
+#pragma clang fp contract(off)
     return __float2int_rz(v + copysignf(0.49999997f, v));
 }
 
@@ -210,6 +213,7 @@ __device__ __forceinline__ void finish_f32(uint8_t *xs, uint8_t *__restrict__ xq
     uint32_t q[4];  // bytes of elements 8h..8h+7 (q[0], q[1]) and 16+8h.. (q[2], q[3])
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+#pragma clang fp contract(off)
         const int32_t a = round_away(v[i].x * d_inv), bb = round_away(v[i].y * d_inv);
         const int32_t c = round_away(v[i].z * d_inv), d = round_away(v[i].w * d_inv);
         q[i] = (uint32_t)(a & 0xff) | ((uint32_t)(bb & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |

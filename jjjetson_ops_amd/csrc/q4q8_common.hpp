@@ -57,6 +57,8 @@ hipError_t launch_moe_gather_q8_1(const void *xq, const int32_t *src_route, void
                                   int top_k, int K, hipStream_t stream);
 hipError_t launch_moe_combine(const float *expert_out, const int32_t *dst_of_route, const float *route_weights,
                               float *y, int num_tokens, int hidden, int top_k, hipStream_t stream);
+// fp32 -> Q4_0 over a flat run of n_blocks 32-value blocks.
+hipError_t launch_quantize_q4_0(const float *w, void *out, int64_t n_blocks, hipStream_t stream);
 hipError_t launch_block_sums(const void *w, const void *xq, int32_t *sumi, int K, int N, int M,
                              hipStream_t stream);
 

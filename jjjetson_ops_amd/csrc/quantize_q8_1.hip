@@ -27,7 +27,9 @@ __device__ __forceinline__ float swz_xor(float v) {
     return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), pattern));
 }
 
+// v0..v3 are the rounded fp32 products x*d_inv (no contraction into what follows).
 __device__ __forceinline__ uint32_t pack_q(float v0, float v1, float v2, float v3) {
+#pragma clang fp contract(off)
     const int32_t a = (int32_t)roundf(v0);
     const int32_t b = (int32_t)roundf(v1);
     const int32_t c = (int32_t)roundf(v2);

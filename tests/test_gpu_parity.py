@@ -200,6 +200,27 @@ def test_fused_quantize_gemv(K, N, dev):
     assert torch.equal(y, y2)
 
 
+@pytest.mark.parametrize("K,N", [(4096, 256), (11008, 64)])
+def test_quantizers_round_the_product_first(K, N, dev):
+    """Crafted activations whose rounded product x*d_inv is a tie k + 0.5 while the
+    exact product lies below it: the fused in-kernel quantizer and the standalone one
+    both give roundf's k + 1 (an unrounded, fused multiply-add would give k)."""
+    import torch
+    from _ties import q8_tie_input
+    note(f"tie-rounding quantizers K={K}")
+    x, slots, qexp = q8_tie_input(K, seed=K)
+    xq_ref = c_oracle.quantize_q8_1(x.reshape(1, K), [K, 1])
+    qs, _, _ = c_oracle.parse_q8_1(xq_ref, K // 128)
+    assert np.array_equal(qs.reshape(-1)[slots].astype(np.int64), qexp)
+    assert np.array_equal(gpu_quantize(x, [K, 1], dev), xq_ref)
+    w = make_w(N, K, 5)
+    xq = torch.zeros(xq_ref.size, dtype=torch.uint8, device=dev)
+    y = torch.empty(N, dtype=torch.float32, device=dev)
+    capi.mat_mul_f32(to_dev(w, dev), to_dev(x, dev), xq, y, K, N, 1)
+    torch.cuda.synchronize()
+    assert np.array_equal(xq.cpu().numpy(), xq_ref)
+
+
 @pytest.mark.parametrize("M", [2, 5])
 def test_f32_entry_batched(M, dev):
     import torch

@@ -439,3 +439,20 @@ def test_moe_combine_closed_forms():
     # top_k = 1 and weight 1: the inverse permutation, exactly
     y1 = oracle_np.moe_combine(eo, dst, np.ones(T * k, np.float32), 1)
     assert np.array_equal(y1, eo[dst])
+
+
+def test_q8_1_tie_inputs_pin_the_rounded_product():
+    """q = roundf(fl(x * d_inv)) (src/cuda/q8_1.cu:71-79): on crafted values whose
+    rounded product is a tie k + 0.5, the oracle gives k + 1 (away from zero), while
+    a fused round-away (the product left unrounded) would give k."""
+    from _ties import q8_tie_input, C_AWAY
+    K = 1024
+    x, slots, qexp = q8_tie_input(K, seed=21)
+    qs, d, s = c_oracle.parse_q8_1(c_oracle.quantize_q8_1(x.reshape(1, K), [K, 1]), K // 128)
+    q = qs.reshape(-1)
+    assert np.array_equal(q[slots].astype(np.int64), qexp)
+    g = x.reshape(-1, 32)
+    dinv = (np.float32(127.0) / np.abs(g).max(axis=1)).astype(np.float32)
+    p = x[slots].astype(np.float64) * dinv[slots // 32].astype(np.float64)
+    fused = np.trunc((p + np.sign(p) * C_AWAY).astype(np.float32)).astype(np.int64)
+    assert np.all(np.abs(fused - qexp) == 1)
