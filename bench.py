@@ -219,6 +219,48 @@ def time_moe_ffn(dev, steps, warmup):
             "mfma_frac": ops / (avg * 1e-3) / 1e12 / INT8_PEAK_TOPS,
             "weight_GBps": wbytes / (avg * 1e-3) / 1e9, "launches_per_step": 8}
 
+def time_quantize_q4_0(dev, steps, warmup, host_threads=16):
+    """The repacker's kernel: fp32 [14336, 4096] -> Q4_0 (one expert's up-projection),
+    inputs rotated over > 512 MB; beside it the host quantizer on the same matrix."""
+    import numpy as np
+    import torch
+    from jjjetson_ops_amd import weights as W
+
+    N, K = 14336, 4096
+    in_bytes = 4 * N * K
+    out_bytes = W.q4_0_bytes(N, K)
+    copies = max(2, math.ceil(ROTATE_BYTES / in_bytes))
+    g = torch.Generator(device=dev).manual_seed(5)
+    w0 = torch.randn(N, K, generator=g, device=dev) * 0.02
+    ws = [w0] + [w0.clone() for _ in range(copies - 1)]
+    outs = [torch.empty(out_bytes, dtype=torch.uint8, device=dev) for _ in range(copies)]
+
+    def step(i):
+        W.quantize_q4_0_device(ws[i % copies], outs[i % copies], N, K)
+
+    for i in range(warmup):
+        step(i)
+    gr = _graph(step, steps)
+    gr.replay()
+    avg = _time_graph(gr) / steps
+    alg = in_bytes + out_bytes
+    res = {"name": "quantize_q4_0_n14336_k4096", "rows": N, "cols": K, "us_per_launch": avg * 1e3,
+           "alg_bytes_per_launch": alg, "GBps": alg / (avg * 1e-3) / 1e9,
+           "hbm_frac": alg / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    wh = w0.cpu().numpy()
+    del gr, ws, outs, w0
+    torch.cuda.empty_cache()
+    if host_threads:
+        t0 = time.perf_counter()
+        n = 0
+        while time.perf_counter() - t0 < 2.0:
+            W.quantize_q4_0(wh, host_threads)
+            n += 1
+        el = (time.perf_counter() - t0) / n
+        res["host_quantizer"] = {"ms": el * 1e3, "GBps": alg / el / 1e9, "threads": host_threads, "runs": n}
+    return res
+
+
 def _traffic(workload):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary (FETCH_SIZE and
     WRITE_SIZE, each scaled by the same counters' reading for a torch copy kernel of
@@ -337,6 +379,8 @@ def main():
             res = time_moe(dev, max(10, args.steps // 10), 3)
         elif args.only == "moe_ffn":
             res = time_moe_ffn(dev, max(5, args.steps // 20), 2)
+        elif args.only == "quantize_q4_0":
+            res = time_quantize_q4_0(dev, max(10, args.steps // 4), 3, host_threads=0)
         else:
             sel = [p for p in plan if p[0] == args.only]
             if not sel:
@@ -369,6 +413,8 @@ def main():
         configs.append(time_moe(dev, max(10, args.steps // 10), 3))
         log("bench: moe ffn")
         configs.append(time_moe_ffn(dev, max(5, args.steps // 20), 2))
+        log("bench: q4_0 repacker kernel")
+        configs.append(time_quantize_q4_0(dev, max(10, args.steps // 4), 3, host_threads=0 if args.no_cpu else 16))
 
     cpu = None
     if not args.no_cpu:
