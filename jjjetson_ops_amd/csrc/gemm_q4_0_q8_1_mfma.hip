@@ -74,6 +74,10 @@ constexpr int kXUnits = kXsBytes / 16;                   // 1152 16-byte units p
 constexpr int kXRuns = kXUnits / 64;                     // 18 wave-sized (1 KB) runs
 
 constexpr uint32_t kBiasBits = 0x4B400000u;              // 1.5 * 2^23
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] + [15:14],
+// expcnt[6:4] = 7, lgkmcnt[11:8] = 15).
+#define JJO_GEMM_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n)&15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
 constexpr float kBias = 12582912.0f;
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -162,9 +166,12 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
         }
     }
     const uint8_t *w_src = w + (size_t)min(n_loc0 + st_row, n_mat - 1) * row_bytes + (size_t)st_half * 36;
-    uint32_t wst[9];                // this thread's 2 raw Q4_0 blocks (36 bytes)
+    // This thread's 2 raw Q4_0 blocks (36 bytes) of a stage, in two register sets:
+    // stage k lands in set k & 1, two compute phases before it is unpacked.
+    uint32_t wr0[9], wr1[9];
 
-    auto load_w = [&](int c) {
+    // Three vector-memory instructions per call (the explicit waits count on it).
+    auto load_w = [&](int c, uint32_t(&wst)[9]) {
         const uint8_t *p = w_src + (size_t)c * (KB * kQ4BlockBytes);
         const u32x4a4 a = *reinterpret_cast<const u32x4a4 *>(p);
         const u32x4a4 b = *reinterpret_cast<const u32x4a4 *>(p + 16);
@@ -183,21 +190,32 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     uint32_t x_off[5];
 #pragma unroll
     for (int i = 0; i < 5; ++i) {
-        const int unit = (wave + 4 * i) * 64 + lane;
+        const int unit = min(wave + 4 * i, kXRuns - 1) * 64 + lane;
         x_off[i] = unit < x_valid_units ? unit * 16 : 0;
     }
+    // Up to five DMA instructions per wave and call (waves 2 and 3 have four runs;
+    // their fifth rewrites run 17 with the same bytes as wave 1).
+    // Issued through inline asm: the compiler's wait insertion cannot tell that the
+    // DMA target (an activation buffer) is disjoint from the weight buffers that the
+    // same iteration writes and reads, and would wait for every load in flight
+    // (vmcnt(0)) before the next LDS access, collapsing the weight prefetch.  Their
+    // completion is waited for explicitly (the vmcnt(3) before each unpack and the
+    // vmcnt(0) after the K loop); the hardware counter counts them like any load.
     auto load_x = [&](int c) {
-        uint8_t *xs = smem + (c & 1) * kXsBytes;
+        const uint32_t xs = (uint32_t)(uintptr_t)(smem + (c & 1) * kXsBytes);
         const uint8_t *src = x_base + (size_t)c * x_stride;
 #pragma unroll
         for (int i = 0; i < 5; ++i) {
-            const int run = wave + 4 * i;
-            if (run < kXRuns)
-                __builtin_amdgcn_global_load_lds((const void *)(src + x_off[i]), (lds_void *)(xs + run * 1024), 16, 0, 0);
+            const int run = min(wave + 4 * i, kXRuns - 1);
+            // Runs past the tile's last token hold nothing a nonzero scale reads
+            // (grouped tails): skipped.  Wave-uniform.
+            if (run * 64 >= x_valid_units) continue;
+            const uint32_t m0v = __builtin_amdgcn_readfirstlane(xs + run * 1024);
+            asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src + x_off[i]), "{m0}"(m0v) : "memory");
         }
     };
 
-    auto store_w = [&](int buf) {
+    auto store_w = [&](int buf, const uint32_t(&wst)[9]) {
         uint8_t *wq = smem + kOffW + buf * kWBufBytes;
         _Float16 *wd_epi = reinterpret_cast<_Float16 *>(wq + kOffWdEpi);
         _Float16 *wd_row = reinterpret_cast<_Float16 *>(wq + kOffWdRow);
@@ -254,22 +272,32 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     // 1): a compile-time parameter of the stage loop below, chosen once per wave.
     const int n_live = (m0 + wm * 64 < m_end) + (m0 + wm * 64 + 32 < m_end);
 
-    // Pipeline, one barrier per stage: while stage c is computed from buffers c&1,
-    // the loads of stage c+1 are in flight; stage c+1's weights are unpacked into the
-    // other buffer right after, then one barrier publishes X(c+1) and W(c+1) and
-    // retires every wave's reads of buffers c&1, which stage c+2's loads then reuse.
+    // Pipeline, one barrier per stage.  While stage c is computed from buffers c&1,
+    // X(c+1) (LDS DMA) and the weights of stages c+1 and c+2 (register sets
+    // (c+1)&1 and c&1) are in flight.  After the compute, W(c+1) is unpacked into
+    // the other weight buffer, one barrier publishes X(c+1) and W(c+1) and retires
+    // the reads of buffers c&1, and then X(c+2) (into buffer c&1) and W(c+3) (into
+    // the set just unpacked) are issued.  Weight loads thus have two compute phases
+    // to land: a grouped GEMM's weight tile is read by one or two workgroups only,
+    // so it comes from HBM, not L2.  The explicit vmcnt(3) before each unpack
+    // covers X(c+1), which was issued after W(c+1): only W(c+2)'s three loads may
+    // still be in flight.
     load_x(0);
-    load_w(0);
-    store_w(0);               // waits for W(0) and, issued before it, X(0)
+    load_w(0, wr0);
+    load_w(min(1, n_stages - 1), wr1);
+    JJO_GEMM_VMCNT(3);
+    store_w(0, wr0);
     __syncthreads();
-    if (n_stages > 1) {
-        load_x(1);
-        load_w(1);
-    }
+    load_x(min(1, n_stages - 1));
+    load_w(min(2, n_stages - 1), wr0);
 
     auto stage_loop = [&](auto live_tag) {
         constexpr int LIVE = decltype(live_tag)::value;
-        for (int c = 0; c < n_stages; ++c) {
+        // One stage; PAR = c & 1 names the register set statically.
+        auto stage = [&](int c, auto par_tag) {
+            constexpr int PAR = decltype(par_tag)::value;
+            uint32_t(&w_next)[9] = *[&]() { if constexpr (PAR) return &wr0; else return &wr1; }();
+
             uint8_t *wq = smem + kOffW + (c & 1) * kWBufBytes;
             const _Float16 *wd_epi = reinterpret_cast<const _Float16 *>(wq + kOffWdEpi);
             const _Float16 *wd_row = reinterpret_cast<const _Float16 *>(wq + kOffWdRow);
@@ -360,16 +388,23 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
             }
             }  // LIVE > 0
 
-            if (c + 1 < n_stages) {
-                store_w((c + 1) & 1);  // waits for W(c+1) and X(c+1), issued a compute phase ago
-                __syncthreads();
-                if (c + 2 < n_stages) {
-                    load_x(c + 2);
-                    load_w(c + 2);
-                }
-            }
+            // Unconditional, also after the last stage (stage indices clamped to the
+            // last one: the extra unpack and loads fill buffers no wave reads any
+            // more): the same number of loads on every path keeps the compiler's
+            // register waits exact instead of vmcnt(0).
+            JJO_GEMM_VMCNT(3);  // all but W(c+2): X(c+1) and W(c+1) have landed
+            store_w((c + 1) & 1, w_next);
+            __syncthreads();
+            load_x(min(c + 2, n_stages - 1));          // buffer c&1, freed by the barrier
+            load_w(min(c + 3, n_stages - 1), w_next);  // set (c+1)&1, just unpacked
+        };
+        int c = 0;
+        for (; c + 1 < n_stages; c += 2) {
+            stage(c, std::integral_constant<int, 0>{});
+            stage(c + 1, std::integral_constant<int, 1>{});
         }
-
+        if (c < n_stages) stage(c, std::integral_constant<int, 0>{});
+        JJO_GEMM_VMCNT(0);  // the clamped loads of the last stage
     };
     if (n_live == 2)
         stage_loop(std::integral_constant<int, 2>{});
