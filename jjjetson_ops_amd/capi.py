@@ -22,6 +22,7 @@ ALGO_AUTO = 0
 ALGO_GEMV = 1
 ALGO_MFMA = 2
 ALGO_SKINNY = 3
+ALGO_SKINNY_LDS = 4
 
 QK = 32
 QSUPER = 128

@@ -1,0 +1,288 @@
+// Small-batch (M <= 16) Q4_0 x Q8_1 matmul on gfx950 int8 matrix cores, with the
+// activation resident in LDS and each workgroup streaming several weight tiles.
+//
+// Math is the reference's per-block epilogue (src/cuda/mm_q4_0_q8_1.cu:71-93):
+//     y[m][n] = sum_b d_w[n,b] * (sumi[n,m,b] * d_x[m,b] - 8 * s_x[m,b])
+// evaluated exactly as in the streaming skinny kernel: v_mfma_i32_16x16x32_i8 with
+// the tokens as MFMA rows and 16 weight rows as columns, the accumulator seeded
+// with the bits of 1.5*2^23 so the result read as fp32 is 1.5*2^23 + sumi, a
+// two-op epilogue (fma with d_x/8, then v_fma_mix with the fp16 d_w), and the
+// -8*s_x term as an f16 MFMA contraction over blocks; y = 8*acc.
+//
+// Layout of the work (one workgroup of 8 waves per CU):
+//   * A workgroup owns T consecutive 16-row weight tiles (T <= 4) and all of K.
+//   * K is walked in windows of up to 4096 values.  The window's Q8_1 activation
+//     (M tokens, the contiguous superblock-major run of the quantizer's layout) is
+//     copied to LDS once per window by all waves; nothing else reads the
+//     activation from L2.
+//   * Wave w takes the window's 256-value stages w, w+8, ...  Per stage it loads
+//     its MFMA activation operands, (d_x/8, -1.5*2^23*d_x/8) and -s_x into
+//     registers once, then runs the stage for every tile of the workgroup.
+//   * Weights stream through a per-wave LDS ring of P items (one item = one stage
+//     of one tile: 16 rows x 144 bytes), in (stage, tile) order, with
+//     global_load_lds_dwordx4 and explicit vmcnt waits; no barrier inside a window.
+//   * The 8 waves' K-slice partials of each tile are added through LDS in wave
+//     order at the end (deterministic).
+//
+// Requirements (checked by the launcher): M <= 16, K % 256 == 0, w and xq 16-byte aligned.
+#include <hip/hip_fp16.h>
+
+#include "q4q8_common.hpp"
+
+namespace jjo {
+namespace {
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kPW = 8;                                   // waves per workgroup
+constexpr int kPStageBlocks = 8;                         // 256 K values per stage
+constexpr int kPRowBytes = kPStageBlocks * kQ4BlockBytes;  // 144
+constexpr int kPItemBytes = 16 * kPRowBytes;             // 2304: one stage of one tile
+constexpr int kPItemChunks = kPItemBytes / 16;           // 144 chunks of 16 bytes
+constexpr int kPRing = 4;                                // items in flight per wave
+constexpr int kPWinK = 4096;                             // K values per activation window
+constexpr int kPMaxTiles = 4;
+constexpr int kPXBytes = (kPWinK / kQSuper) * 16 * kQ8BlockBytes;   // 73728 (M = 16)
+constexpr int kPRingBytes = kPW * kPRing * kPItemBytes;             // 73728
+constexpr int kPSmemBytes = kPXBytes + kPRingBytes;                 // 147456
+constexpr uint32_t kPBiasBits = 0x4B400000u;  // 1.5 * 2^23
+constexpr float kPBias = 12582912.0f;
+
+static_assert(kPW * kPMaxTiles * 64 * 16 <= kPSmemBytes, "reduction area must fit");
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] + [15:14],
+// expcnt[6:4] = 7, lgkmcnt[11:8] = 15).
+#define JJO_P_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n)&15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+__device__ __forceinline__ void p_vm_wait(int n) {  // n wave-uniform, 0..12
+    switch (n) {
+        case 0: JJO_P_VMCNT(0); break;
+        case 1: JJO_P_VMCNT(1); break;
+        case 2: JJO_P_VMCNT(2); break;
+        case 3: JJO_P_VMCNT(3); break;
+        case 4: JJO_P_VMCNT(4); break;
+        case 5: JJO_P_VMCNT(5); break;
+        case 6: JJO_P_VMCNT(6); break;
+        case 7: JJO_P_VMCNT(7); break;
+        case 8: JJO_P_VMCNT(8); break;
+        case 9: JJO_P_VMCNT(9); break;
+        case 10: JJO_P_VMCNT(10); break;
+        case 11: JJO_P_VMCNT(11); break;
+        case 12: JJO_P_VMCNT(12); break;
+        default: JJO_P_VMCNT(0); break;
+    }
+}
+
+// 16 bytes per lane, global -> LDS at m0 + 16*lane.  Inline asm so that the
+// compiler's wait insertion does not treat the ring writes as aliasing every other
+// LDS access (it would wait for all loads in flight); completion is waited for
+// explicitly.
+__device__ __forceinline__ void dma16(const void *src, uint32_t lds_base) {
+    asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds_base))
+                 : "memory");
+}
+
+__global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uint8_t *__restrict__ w,
+                                                                        const uint8_t *__restrict__ xq,
+                                                                        float *__restrict__ y, int K, int N, int M,
+                                                                        int tiles_per_wg) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint8_t *xs = smem;                     // activation window [K/128][M][144]
+    uint8_t *ring_all = smem + kPXBytes;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l16 = lane & 15;
+    const int g = lane >> 4;
+    const int nb = K / kQK;
+    const size_t row_bytes = (size_t)nb * kQ4BlockBytes;
+    const int n_tiles_total = (N + 15) / 16;
+    const int tile0 = blockIdx.x * tiles_per_wg;
+    const int T = max(0, min(tiles_per_wg, n_tiles_total - tile0));  // workgroup-uniform
+    uint8_t *ring = ring_all + wave * (kPRing * kPItemBytes);
+
+    i32x4 bias;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bias[i] = (int32_t)kPBiasBits;
+    asm volatile("" : "+v"(bias));
+
+    f32x4 acc[kPMaxTiles];
+#pragma unroll
+    for (int t = 0; t < kPMaxTiles; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // token row this lane feeds to the MFMA (clamped: rows >= M are never stored)
+    const int tok = min(l16, M - 1);
+
+    for (int k0 = 0; k0 < K; k0 += kPWinK) {
+        const int win = min(kPWinK, K - k0);
+        const int n_st = win / (kPStageBlocks * kQK);   // stages in the window
+        // ---- activation window -> LDS (all waves), contiguous bytes ----
+        {
+            const int xbytes = (win / kQSuper) * M * kQ8BlockBytes;
+            const uint8_t *src = xq + (size_t)(k0 / kQSuper) * M * kQ8BlockBytes;
+            const int n_chunks = xbytes / 16;
+            for (int c0 = wave * 64; c0 < n_chunks; c0 += kPW * 64) {
+                const int c = c0 + lane;
+                if (c < n_chunks) dma16(src + 16 * (size_t)c, (uint32_t)(uintptr_t)(xs + 16 * c0));
+            }
+            JJO_P_VMCNT(0);
+            __syncthreads();
+        }
+        const int x_stride_sb = M * kQ8BlockBytes;  // bytes per superblock in the window
+
+        // ---- this wave's items: (stage s = wave + 8j, tile t) in (s, t) order ----
+        const int my_st = (n_st - wave + kPW - 1) / kPW;
+        const int n_items = my_st * T;
+        auto issue = [&](int it) {
+            const int j = it / T, t = it - j * T;
+            const int s = wave + kPW * j;
+            uint8_t *slot = ring + (it % kPRing) * kPItemBytes;
+            const uint8_t *base = w + (size_t)((k0 / kQK) + s * kPStageBlocks) * kQ4BlockBytes;
+            // Three DMA instructions per item (the third with lanes 0..15 only): chunk
+            // c = 64*i + lane -> row c / 9, 16-byte piece c % 9 of the row's 144 bytes,
+            // i.e. LDS slot offset 16*c.  Rows past N re-read row N-1 (never stored).
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                const int c = min(64 * i + lane, kPItemChunks - 1);
+                const int r = min((tile0 + t) * 16 + c / 9, N - 1);
+                const uint8_t *src = base + (size_t)r * row_bytes + 16u * (uint32_t)(c % 9);
+                if (i < 2 || lane < kPItemChunks - 128) dma16(src, (uint32_t)(uintptr_t)(slot + 1024 * i));
+            }
+        };
+        const int pre = min(kPRing, n_items);
+        for (int it = 0; it < pre; ++it) issue(it);
+
+        for (int j = 0; j < my_st; ++j) {
+            const int s = wave + kPW * j;
+            // stage operands from the activation window (registers, reused for all tiles)
+            const uint8_t *xst = xs + (size_t)(s * 2) * x_stride_sb;  // 2 superblocks per stage
+            long aop[kPStageBlocks];
+            f32x4 dx8[kPStageBlocks], nb8[kPStageBlocks];
+            f16x4 sx_op;
+            {
+#pragma unroll
+                for (int bb = 0; bb < kPStageBlocks; ++bb) {
+                    const int h = bb >> 2, jj = bb & 3;
+                    const uint32_t *qa = reinterpret_cast<const uint32_t *>(xst + h * x_stride_sb +
+                                                                            tok * kQ8BlockBytes + 16 + 32 * jj + 4 * g);
+                    aop[bb] = (long)((uint64_t)qa[4] << 32 | qa[0]);
+                }
+                // d_x of tokens 4g..4g+3 (the output rows of this lane)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int m = min(4 * g + i, M - 1);
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const uint4 v = *reinterpret_cast<const uint4 *>(xst + h * x_stride_sb + m * kQ8BlockBytes);
+                        const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                        for (int jj = 0; jj < 4; ++jj) {
+                            const float d8 = __half2float(__ushort_as_half((unsigned short)(vv[jj] & 0xffffu))) * 0.125f;
+                            dx8[4 * h + jj][i] = d8;
+                            nb8[4 * h + jj][i] = -kPBias * d8;
+                        }
+                    }
+                }
+                // -s_x of the stage's 8 blocks as the f16 A operand of the s_x MFMA:
+                // lane (token l16, group g < 2) holds blocks 4g..4g+3; groups 2, 3 are zero.
+                const uint4 v = *reinterpret_cast<const uint4 *>(xst + (g & 1) * x_stride_sb + tok * kQ8BlockBytes);
+                const uint32_t keep = g < 2 ? 0xffffffffu : 0u;
+                const uint32_t lo = (__builtin_amdgcn_perm(v.y, v.x, 0x07060302u) ^ 0x80008000u) & keep;
+                const uint32_t hi = (__builtin_amdgcn_perm(v.w, v.z, 0x07060302u) ^ 0x80008000u) & keep;
+                sx_op = __builtin_bit_cast(f16x4, (uint64_t)hi << 32 | lo);
+            }
+#pragma unroll
+            for (int t = 0; t < kPMaxTiles; ++t) {
+                if (t >= T) break;  // workgroup-uniform
+                // one tile at a time: no hoisting of the next tile's operand reads
+                __builtin_amdgcn_sched_barrier(0);
+                const int it = j * T + t;
+                p_vm_wait(3 * (min(kPRing, n_items - it) - 1));
+                const uint8_t *slot = ring + (it % kPRing) * kPItemBytes;
+                const uint8_t *wr0 = slot + l16 * kPRowBytes;
+                // s_x term: d_w of blocks 4(g&1)..4(g&1)+3 of this lane's weight row
+                {
+                    const _Float16 *dr = reinterpret_cast<const _Float16 *>(wr0 + (g & 1) * 4 * kQ4BlockBytes);
+                    f16x4 dw_op;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) dw_op[q] = dr[q * kQ4BlockBytes / 2];
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(sx_op, dw_op, acc[t], 0, 0, 0);
+                }
+#pragma unroll
+                for (int bb = 0; bb < kPStageBlocks; ++bb) {
+                    const uint8_t *wr = wr0 + bb * kQ4BlockBytes;
+                    uint32_t q;
+                    if ((bb & 1) == 0) {  // nibble dword g at 2 mod 4: re-align
+                        const uint32_t *p = reinterpret_cast<const uint32_t *>(wr + 4 * g);
+                        q = __builtin_amdgcn_alignbyte(p[1], p[0], 2);
+                    } else {
+                        q = *reinterpret_cast<const uint32_t *>(wr + 2 + 4 * g);
+                    }
+                    const _Float16 dw = *reinterpret_cast<const _Float16 *>(wr);
+                    const long bop = (long)((uint64_t)((q >> 4) & 0x0f0f0f0fu) << 32 | (q & 0x0f0f0f0fu));
+                    const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop[bb], bop, bias, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float tt = fmaf(__int_as_float(d[i]), dx8[bb][i], nb8[bb][i]);
+                        acc[t][i] = fmaf((float)dw, tt, acc[t][i]);
+                    }
+                }
+                // slot it % P fully read (lgkmcnt(0)) before it is refilled
+                if (it + kPRing < n_items) {
+                    __builtin_amdgcn_s_waitcnt(0xC07F);
+                    issue(it + kPRing);
+                }
+            }
+        }
+        JJO_P_VMCNT(0);
+        __syncthreads();  // the window's activation and the rings are free again
+    }
+
+    // ---- K-slice partials of each tile -> LDS, summed in wave order ----
+    f32x4 *red = reinterpret_cast<f32x4 *>(smem);
+#pragma unroll
+    for (int t = 0; t < kPMaxTiles; ++t)
+        if (t < T) red[(t * kPW + wave) * 64 + lane] = acc[t];
+    __syncthreads();
+    if (wave < T) {
+        const int t = wave;
+        f32x4 sum = red[(t * kPW + 0) * 64 + lane];
+#pragma unroll
+        for (int k = 1; k < kPW; ++k) sum = sum + red[(t * kPW + k) * 64 + lane];
+        const int n = (tile0 + t) * 16 + l16;
+        if (n < N) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = 4 * g + i;
+                if (m < M) y[(size_t)m * N + n] = 8.0f * sum[i];
+            }
+        }
+    }
+}
+
+}  // namespace
+
+bool gemm_skinny_persist_supported(const void *w, const void *xq, int K, int M) {
+    return K % 256 == 0 && M >= 1 && M <= 16 && ((uintptr_t)w & 15) == 0 && ((uintptr_t)xq & 15) == 0;
+}
+
+hipError_t launch_gemm_skinny_persist(const void *w, const void *xq, float *y, int K, int N, int M,
+                                      hipStream_t stream) {
+    if (!gemm_skinny_persist_supported(w, xq, K, M)) return hipErrorInvalidValue;
+    static bool attr_done = false;
+    if (!attr_done) {
+        hipError_t e = hipFuncSetAttribute((const void *)gemm_skinny_persist_kernel,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kPSmemBytes);
+        if (e != hipSuccess) return e;
+        attr_done = true;
+    }
+    const int n_tiles = (N + 15) / 16;
+    const int tiles_per_wg = min(kPMaxTiles, (n_tiles + 255) / 256);
+    const int blocks = (n_tiles + tiles_per_wg - 1) / tiles_per_wg;
+    hipLaunchKernelGGL(gemm_skinny_persist_kernel, dim3(blocks), dim3(64 * kPW), kPSmemBytes, stream,
+                       (const uint8_t *)w, (const uint8_t *)xq, y, K, N, M, tiles_per_wg);
+    return hipGetLastError();
+}
+
+}  // namespace jjo

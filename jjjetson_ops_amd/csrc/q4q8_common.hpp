@@ -41,6 +41,10 @@ hipError_t launch_gemv_fused(const void *w, const float *x, void *xq_out, float 
 bool gemm_skinny_supported(const void *w, const void *xq, int K, int M);
 hipError_t launch_gemm_skinny(const void *w, const void *xq, float *y, int K, int N, int M,
                               hipStream_t stream);
+// Batch <= 16: activation resident in LDS, up to 4 weight tiles per workgroup.
+bool gemm_skinny_persist_supported(const void *w, const void *xq, int K, int M);
+hipError_t launch_gemm_skinny_persist(const void *w, const void *xq, float *y, int K, int N, int M,
+                                      hipStream_t stream);
 hipError_t launch_gemm_mfma(const void *w, const void *xq, float *y, int K, int N, int M,
                             hipStream_t stream);
 hipError_t launch_gemm_mfma_grouped(const void *w, const void *xq, const int32_t *expert_offsets,

@@ -165,6 +165,42 @@ def test_gemm_skinny(K, N, M, dev):
     np.testing.assert_allclose(got, c_oracle.matmul(w, xq, K, N, M), rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("M", [1, 3, 4, 8, 13, 16])
+@pytest.mark.parametrize("K,N", [(4096, 257), (11008, 64), (256, 5), (768, 96), (14336, 48), (4352, 257),
+                                 (4096, 4100), (512, 16400)])
+def test_gemm_skinny_lds(K, N, M, dev):
+    """The LDS-resident skinny kernel: K windows of 4096 (14336 = 3.5 windows, 4352 =
+    a one-stage last window), 1..4 tiles per workgroup (N=4100: 2, N=16400: 4 with a
+    second round), rows and tokens past the end."""
+    note(f"gemm skinny lds K={K} N={N} M={M}")
+    w = make_w(N, K, 13 * N + K)
+    x = make_x(K, M, 400 + M)
+    xq = c_oracle.quantize_q8_1(x, [K, M])
+    got = run_mm(w, xq, K, N, M, capi.ALGO_SKINNY_LDS, dev)
+    np.testing.assert_allclose(got, c_oracle.matmul(w, xq, K, N, M), rtol=RTOL, atol=ATOL)
+
+
+def test_gemm_skinny_lds_full_size(dev):
+    """BASELINE config 3 at M=16 (K=4096, N=14336: four tiles per workgroup)."""
+    K, N, M = 4096, 14336, 16
+    note(f"gemm skinny lds full size K={K} N={N} M={M}")
+    w = make_w(N, K, 2)
+    x = make_x(K, M, 16)
+    xq = c_oracle.quantize_q8_1(x, [K, M])
+    got = run_mm(w, xq, K, N, M, capi.ALGO_SKINNY_LDS, dev)
+    np.testing.assert_allclose(got, c_oracle.matmul(w, xq, K, N, M), rtol=RTOL, atol=ATOL)
+
+
+def test_gemm_skinny_lds_rejects_unsupported(dev):
+    import torch
+    for K, M in ((640, 4), (4096, 17)):
+        w = torch.zeros(8 * K // 32 * 18, dtype=torch.uint8, device=dev)
+        xq = torch.zeros(M * K // 128 * 144, dtype=torch.uint8, device=dev)
+        y = torch.empty(M * 8, dtype=torch.float32, device=dev)
+        with pytest.raises(RuntimeError, match="LDS-resident skinny"):
+            capi.mat_mul(w, xq, y, K, 8, M, algo=capi.ALGO_SKINNY_LDS)
+
+
 def test_gemm_skinny_rejects_unsupported(dev):
     """K % 256 != 0 and batch > 32 are refused with an error, not computed."""
     import torch
