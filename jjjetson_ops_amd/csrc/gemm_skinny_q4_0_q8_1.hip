@@ -195,6 +195,9 @@ __global__ __launch_bounds__(64 * KW) void gemm_skinny_kernel(const uint8_t *__r
                 row[16 * CT + m] = -kBias * dx8;
             }
         }
+        // The table is written as floats and read below as float4: keep type-based
+        // alias analysis from moving those reads above these writes.
+        asm volatile("" ::: "memory");
         // -s_x of the stage's 8 blocks as the f16 A operand of the s_x MFMA: lane
         // (token l16, group g < 2) holds blocks 4g..4g+3; groups 2, 3 are zero.
         f16x4 sx_op[CT];
