@@ -425,7 +425,7 @@ def main():
     # (only) kernel, and its average duration is the step's.
     roof = {"bound": "hbm", "achieved": head["step_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": head["step_GBps"] / HBM_PEAK_GBS, "traffic": _traffic("gemv_m1_k4096_n11008"),
-            "kernel": "gemv_q4_0_q8_1_kernel<1,2,1,8,fused,1>", "alg_bytes_per_launch": head["step_alg_bytes"],
+            "kernel": "gemv_q4_0_q8_1_kernel<1,4,1,4,fused,1>", "alg_bytes_per_launch": head["step_alg_bytes"],
             "kernel_us_avg": head["us_per_step"],
             "timing": "HIP graph of back-to-back launches on the launch stream, torch.cuda.Event around the replay",
             "q8_1_input_kernel": {"kernel": "gemv_q4_0_q8_1_kernel<1,2,1,8,q8_1,1>",

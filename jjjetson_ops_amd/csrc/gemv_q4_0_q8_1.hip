@@ -413,15 +413,26 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
 #ifndef JJO_GEMV4_U
 #define JJO_GEMV4_U 4
 #endif
-template <int M, int JS>
+// The fused decode step (fp32 x quantized in every workgroup) prefers fewer,
+// deeper workgroups: four rows per wave, four row groups (K <= 4096), which halves
+// the workgroups that re-read and re-quantize x (7.22 against 7.44 us at K=4096,
+// N=11008 on one box; the Q8_1-input kernel is faster with two rows per wave).
+#ifndef JJO_GEMV1F_U
+#define JJO_GEMV1F_U 4
+#endif
+#ifndef JJO_GEMV1F_RG1
+#define JJO_GEMV1F_RG1 4
+#endif
+template <int M, int JS, bool FUSED = false>
 constexpr int rg_for() {
+    if (M == 1 && FUSED && JS == 1) return JJO_GEMV1F_RG1;
     if (M == 1) return JS == 1 ? JJO_GEMV1_RG1 : JS == 2 ? 4 : JS == 3 ? JJO_GEMV1_RG3 : 2;
     return JS == 1 ? JJO_GEMVM_RG1 : JS == 2 ? 2 : 1;
 }
 
 template <int M, int U, int JS, bool FUSED, int EARLY>
 hipError_t launch_cfg(const void *w, const void *xin, uint8_t *xq_out, float *y, int K, int N, hipStream_t stream) {
-    constexpr int RG = rg_for<M, JS>();
+    constexpr int RG = rg_for<M, JS, FUSED>();
     const int groups = (N + U - 1) / U;
     const int blocks = (groups + RG - 1) / RG;
     const size_t smem = ((size_t)M * (K / 64) + 1) * kRec;
@@ -442,7 +453,7 @@ hipError_t launch_cfg(const void *w, const void *xin, uint8_t *xq_out, float *y,
 
 template <int M, int U, int JS, bool FUSED>
 hipError_t launch_js(const void *w, const void *xin, uint8_t *xq_out, float *y, int K, int N, hipStream_t stream) {
-    constexpr int RG = rg_for<M, JS>();
+    constexpr int RG = rg_for<M, JS, FUSED>();
     const int n_items = FUSED ? 2 * (K / kQK) : M * (K / kQK);
     const int rounds = (n_items + 64 * JS * RG - 1) / (64 * JS * RG);
     if (rounds <= 1) return launch_cfg<M, U, JS, FUSED, 1>(w, xin, xq_out, y, K, N, stream);
@@ -482,7 +493,7 @@ hipError_t launch_gemv_dot4(const void *w, const void *xq, float *y, int K, int 
 
 hipError_t launch_gemv_fused(const void *w, const float *x, void *xq_out, float *y, int K, int N,
                              hipStream_t stream) {
-    return launch_m<1, JJO_GEMV1_U, true>(w, x, (uint8_t *)xq_out, y, K, N, stream);
+    return launch_m<1, JJO_GEMV1F_U, true>(w, x, (uint8_t *)xq_out, y, K, N, stream);
 }
 
 }  // namespace jjo
