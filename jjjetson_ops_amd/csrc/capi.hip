@@ -35,6 +35,25 @@ int hip_fail(hipError_t e, const char *what) {
     return set_error(JJO_ERR_HIP, "%s failed: %s", what, hipGetErrorString(e));
 }
 
+hipError_t ensure_dynamic_lds(const void *kernel, size_t bytes) {
+    static std::mutex mu;
+    static std::vector<std::pair<std::pair<const void *, int>, size_t>> granted;  // (kernel, device) -> bytes
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lk(mu);
+    for (auto &g : granted)
+        if (g.first.first == kernel && g.first.second == dev) {
+            if (g.second >= bytes) return hipSuccess;
+            e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+            if (e == hipSuccess) g.second = bytes;
+            return e;
+        }
+    e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e == hipSuccess) granted.push_back({{kernel, dev}, bytes});
+    return e;
+}
+
 namespace {
 
 // The current device must be a gfx950 (MI355X-class) part: every kernel here is

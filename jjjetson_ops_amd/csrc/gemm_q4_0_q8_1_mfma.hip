@@ -447,14 +447,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
 
 template <bool kGrouped>
 hipError_t set_smem_attr() {
-    static bool done = false;
-    if (!done) {
-        hipError_t e = hipFuncSetAttribute((const void *)gemm_q4_0_q8_1_mfma_kernel<kGrouped>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kSmemBytes);
-        if (e != hipSuccess) return e;
-        done = true;
-    }
-    return hipSuccess;
+    return ensure_dynamic_lds((const void *)gemm_q4_0_q8_1_mfma_kernel<kGrouped>, kSmemBytes);
 }
 
 }  // namespace

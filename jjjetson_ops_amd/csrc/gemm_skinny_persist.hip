@@ -270,13 +270,8 @@ bool gemm_skinny_persist_supported(const void *w, const void *xq, int K, int M) 
 hipError_t launch_gemm_skinny_persist(const void *w, const void *xq, float *y, int K, int N, int M,
                                       hipStream_t stream) {
     if (!gemm_skinny_persist_supported(w, xq, K, M)) return hipErrorInvalidValue;
-    static bool attr_done = false;
-    if (!attr_done) {
-        hipError_t e = hipFuncSetAttribute((const void *)gemm_skinny_persist_kernel,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kPSmemBytes);
-        if (e != hipSuccess) return e;
-        attr_done = true;
-    }
+    hipError_t e = ensure_dynamic_lds((const void *)gemm_skinny_persist_kernel, kPSmemBytes);
+    if (e != hipSuccess) return e;
     const int n_tiles = (N + 15) / 16;
     const int tiles_per_wg = min(kPMaxTiles, (n_tiles + 255) / 256);
     const int blocks = (n_tiles + tiles_per_wg - 1) / tiles_per_wg;

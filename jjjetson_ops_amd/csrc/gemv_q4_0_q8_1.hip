@@ -438,13 +438,8 @@ hipError_t launch_cfg(const void *w, const void *xin, uint8_t *xq_out, float *y,
     const size_t smem = ((size_t)M * (K / 64) + 1) * kRec;
     if (smem > 64 * 1024) {
         // Raise this instantiation's dynamic-LDS limit to what the call needs.
-        static size_t granted = 64 * 1024;
-        if (smem > granted) {
-            hipError_t e = hipFuncSetAttribute((const void *)gemv_q4_0_q8_1_kernel<M, U, JS, RG, FUSED, EARLY>,
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
-            if (e != hipSuccess) return e;
-            granted = smem;
-        }
+        hipError_t e = ensure_dynamic_lds((const void *)gemv_q4_0_q8_1_kernel<M, U, JS, RG, FUSED, EARLY>, smem);
+        if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL((gemv_q4_0_q8_1_kernel<M, U, JS, RG, FUSED, EARLY>), dim3(blocks), dim3(64 * JS * RG), smem,
                        stream, (const uint8_t *)w, xin, xq_out, y, K, N);

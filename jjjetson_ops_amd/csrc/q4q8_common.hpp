@@ -27,6 +27,11 @@ int hip_fail(hipError_t e, const char *what);
         if (jjo_e_ != hipSuccess) return ::jjo::hip_fail(jjo_e_, #expr); \
     } while (0)
 
+// Raises `kernel`'s dynamic-LDS limit to at least `bytes` on the current device
+// (hipFuncAttributeMaxDynamicSharedMemorySize), once per (kernel, device) and
+// thread-safely; later calls with the same or a smaller size cost a lookup.
+hipError_t ensure_dynamic_lds(const void *kernel, size_t bytes);
+
 // Kernel launchers (asynchronous on `stream`).  Shapes are validated by the
 // C-ABI layer before these are called.
 hipError_t launch_quantize_q8_1(const float *x, void *y, int64_t K, int64_t ne1, int64_t nz,
