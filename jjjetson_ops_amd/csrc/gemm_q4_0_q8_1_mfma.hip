@@ -266,8 +266,16 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     // re-materialized (16 v_mov) before every MFMA whose result reuses them.
     asm volatile("" : "+v"(bias));
 
-    // Columns past m_end hold stale LDS bytes: their scales are forced to zero.
-    const bool col_ok[2] = {m0 + wm * 64 + l32 < m_end, m0 + wm * 64 + 32 + l32 < m_end};
+    // Tokens past m_end (a tail tile) hold stale LDS bytes: once an activation tile has
+    // landed, their (d, s) headers are zeroed, so every product with them is zero.
+    const int x_valid_tokens = min(BM, m_end - m0);
+    auto zero_tail_headers = [&](int buf) {
+        if (x_valid_tokens < BM) {  // uniform over the workgroup
+            if (tid >= x_valid_tokens && tid < BM)
+                *reinterpret_cast<u32x4 *>(smem + buf * kXsBytes + tid * kQ8BlockBytes) = u32x4{0u, 0u, 0u, 0u};
+            __syncthreads();
+        }
+    };
     // 32-token sub-tiles of this wave that hold valid tokens (grouped tails have 0 or
     // 1): a compile-time parameter of the stage loop below, chosen once per wave.
     const int n_live = (m0 + wm * 64 < m_end) + (m0 + wm * 64 + 32 < m_end);
@@ -288,6 +296,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     JJO_GEMM_VMCNT(3);
     store_w(0, wr0);
     __syncthreads();
+    zero_tail_headers(0);
     load_x(min(1, n_stages - 1));
     load_w(min(2, n_stages - 1), wr0);
 
@@ -309,8 +318,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
             for (int ct = 0; ct < 2; ++ct) {
                 const int col = wm * 64 + ct * 32 + l32;
                 const u32x4 h = *reinterpret_cast<const u32x4 *>(xs + col * kQ8BlockBytes);
-                hdr[ct][0] = col_ok[ct] ? h.x : 0u; hdr[ct][1] = col_ok[ct] ? h.y : 0u;
-                hdr[ct][2] = col_ok[ct] ? h.z : 0u; hdr[ct][3] = col_ok[ct] ? h.w : 0u;
+                hdr[ct][0] = h.x; hdr[ct][1] = h.y; hdr[ct][2] = h.z; hdr[ct][3] = h.w;
             }
 
             if constexpr (LIVE > 0) {
@@ -330,9 +338,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
                 float dx8[2], nb8[2];
     #pragma unroll
                 for (int ct = 0; ct < 2; ++ct) {
-                    const float dx = __half2float(__ushort_as_half((unsigned short)(hdr[ct][b] & 0xffffu)));
-                    dx8[ct] = dx * 0.125f;
-                    nb8[ct] = -kBias * dx8[ct];
+                    // From the fp16 bits (low half): d_x/8 and -1.5*2^23*d_x/8.
+                    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(dx8[ct]) : "v"(hdr[ct][b]), "s"(0.125f));
+                    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(nb8[ct]) : "v"(hdr[ct][b]), "s"(-kBias * 0.125f));
                 }
                 uint32_t wv[2][8];
     #pragma unroll
@@ -376,6 +384,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
                     const uint32_t *h = hdr[ct];
                     uint32_t lo = ((h[0] >> 16) | (h[1] & 0xffff0000u)) ^ 0x80008000u;
                     uint32_t hi = ((h[2] >> 16) | (h[3] & 0xffff0000u)) ^ 0x80008000u;
+                    // Zero B (not A) in the upper K half: an infinite s_x must not meet 0.
                     if (hh) { lo = 0u; hi = 0u; }
                     const u32x2 pk = {lo, hi};
                     bop[ct] = __builtin_bit_cast(f16x4, pk);
@@ -395,6 +404,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
             JJO_GEMM_VMCNT(3);  // all but W(c+2): X(c+1) and W(c+1) have landed
             store_w((c + 1) & 1, w_next);
             __syncthreads();
+            zero_tail_headers((c + 1) & 1);
             load_x(min(c + 2, n_stages - 1));          // buffer c&1, freed by the barrier
             load_w(min(c + 3, n_stages - 1), w_next);  // set (c+1)&1, just unpacked
         };

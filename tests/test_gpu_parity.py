@@ -294,6 +294,26 @@ def test_zero_activation_group_gives_nan_like_reference(dev):
     assert np.all(np.isnan(y.cpu().numpy()))
 
 
+@pytest.mark.parametrize("M", [2, 6, 70])
+def test_infinite_block_sum_gives_inf_like_reference(M, dev):
+    """A block whose fp16 sum term s overflows to inf: the reference's
+    d_w * (d_x * sumi - 8 * s) is +-inf for every output row of that token."""
+    K, N = 256, 64
+    note(f"infinite s block M={M}")
+    w = make_w(N, K, 9)
+    x = make_x(K, M, 9)
+    x[1, 64:96] = 3000.0   # d = 3000/127, sum q = 4064 -> s = 96000 -> inf in fp16
+    xq = c_oracle.quantize_q8_1(x, [K, M])
+    exp = c_oracle.matmul(w, xq, K, N, M)
+    assert np.all(np.isinf(exp[1]))
+    algos = [capi.ALGO_MFMA] + ([capi.ALGO_GEMV] if M <= 8 else []) + ([capi.ALGO_SKINNY] if M <= 32 else [])
+    algos += [capi.ALGO_SKINNY_LDS] if M <= 16 else []
+    for algo in algos:
+        got = run_mm(w, xq, K, N, M, algo, dev)
+        assert np.array_equal(got[1], exp[1]), algo
+        np.testing.assert_allclose(np.delete(got, 1, 0), np.delete(exp, 1, 0), rtol=RTOL, atol=ATOL)
+
+
 def test_mmq_host_entry_through_pybind(dev):
     """mm_q4_0_q8_1_me.mmq: quant_workspace bit-exact, output within tolerance."""
     import mm_q4_0_q8_1_me
@@ -355,7 +375,7 @@ def _sample_check(w, xq, y, K, N, M, n_rows=96, n_tok=64, seed=0):
 
 
 @pytest.mark.parametrize("K,N,M,seed", [(4096, 11008, 1, 1), (11008, 4096, 1, 1), (4096, 14336, 8, 2),
-                                        (4096, 14336, 16, 2), (4096, 4096, 2048, 3)])
+                                        (4096, 14336, 16, 2), (4096, 4096, 2048, 3), (4096, 14336, 2048, 3)])
 def test_baseline_configs_sampled(K, N, M, seed, dev):
     import torch
     note(f"baseline config K={K} N={N} M={M}")
@@ -376,3 +396,4 @@ def test_baseline_configs_sampled(K, N, M, seed, dev):
     assert np.array_equal(xq.reshape(K // 128, M, 144)[:, toks].reshape(-1),
                           c_oracle.quantize_q8_1(x[toks], [K, toks.size]))
     _sample_check(w, xq, y.cpu().numpy().reshape(M, N), K, N, M, seed=seed)
+
