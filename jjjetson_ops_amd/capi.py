@@ -23,6 +23,7 @@ ALGO_GEMV = 1
 ALGO_MFMA = 2
 ALGO_SKINNY = 3
 ALGO_SKINNY_LDS = 4
+ALGO_MFMA64 = 5
 
 QK = 32
 QSUPER = 128

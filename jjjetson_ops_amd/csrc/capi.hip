@@ -56,27 +56,39 @@ hipError_t ensure_dynamic_lds(const void *kernel, size_t bytes) {
 
 namespace {
 
+std::mutex g_dev_mu;
+std::vector<int> g_dev_cus;  // compute units per device, filled by require_gfx950
+
 // The current device must be a gfx950 (MI355X-class) part: every kernel here is
 // built for that ISA only.  Checked once per device and cached.
 int require_gfx950() {
-    static std::mutex mu;
     static std::vector<int> state;  // 0 unknown, 1 ok, 2 bad
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return set_error(JJO_ERR_NO_DEVICE, "no HIP device: %s", hipGetErrorString(e));
-    std::lock_guard<std::mutex> lk(mu);
+    std::lock_guard<std::mutex> lk(g_dev_mu);
     if ((int)state.size() <= dev) state.resize(dev + 1, 0);
     if (state[dev] == 0) {
         hipDeviceProp_t prop;
         e = hipGetDeviceProperties(&prop, dev);
         if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
         state[dev] = strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 2;
+        if ((int)g_dev_cus.size() <= dev) g_dev_cus.resize(dev + 1, 0);
+        g_dev_cus[dev] = prop.multiProcessorCount;
         if (state[dev] == 2)
             return set_error(JJO_ERR_NO_DEVICE, "device %d is %s; this library is built for gfx950 only",
                              dev, prop.gcnArchName);
     }
     if (state[dev] != 1) return set_error(JJO_ERR_NO_DEVICE, "device %d is not gfx950", dev);
     return JJO_OK;
+}
+
+// Compute units of the current device (after require_gfx950 succeeded on it).
+int device_cus() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> lk(g_dev_mu);
+    return dev < (int)g_dev_cus.size() && g_dev_cus[dev] > 0 ? g_dev_cus[dev] : 256;
 }
 
 struct Dims {
@@ -151,8 +163,15 @@ int run_mm(const void *w, const void *xq, float *y, int K, int N, int M, int alg
             algo = JJO_ALGO_SKINNY_LDS;
         else if (gemm_skinny_supported(w, xq, K, M))
             algo = JJO_ALGO_SKINNY;
+        else if (gemv_ok)
+            algo = JJO_ALGO_GEMV;
+        // The 128 x 128 tiles fill the chip only from about 1.5 tiles per CU; below
+        // that the 64 x 64 kernel runs four times as many workgroups and is up to 2x
+        // faster (K=4096: N=14336 up to M=384, N=4096 up to M=1024).
+        else if (2 * (int64_t)((N + 127) / 128) * ((M + 127) / 128) < 3 * (int64_t)device_cus())
+            algo = JJO_ALGO_MFMA64;
         else
-            algo = gemv_ok ? JJO_ALGO_GEMV : JJO_ALGO_MFMA;
+            algo = JJO_ALGO_MFMA;
     }
     hipError_t e;
     if (algo == JJO_ALGO_GEMV) {
@@ -178,6 +197,10 @@ int run_mm(const void *w, const void *xq, float *y, int K, int N, int M, int alg
                              "weights (batch=%d K=%d)", M, K);
         e = launch_gemm_skinny_persist(w, xq, y, K, N, M, s);
         if (e != hipSuccess) return hip_fail(e, "gemm_skinny_persist launch");
+    } else if (algo == JJO_ALGO_MFMA64) {
+        if ((M + 63) / 64 > 65535) return set_error(JJO_ERR_INVALID_ARG, "batch too large");
+        e = launch_gemm_mfma64(w, xq, y, K, N, M, s);
+        if (e != hipSuccess) return hip_fail(e, "gemm_q4_0_q8_1_mfma64 launch");
     } else if (algo == JJO_ALGO_MFMA) {
         if ((M + 127) / 128 > 65535) return set_error(JJO_ERR_INVALID_ARG, "batch too large");
         e = launch_gemm_mfma(w, xq, y, K, N, M, s);

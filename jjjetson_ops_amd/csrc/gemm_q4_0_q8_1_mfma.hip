@@ -38,20 +38,11 @@
 
 #include <type_traits>
 
+#include "mfma_q4q8_tile.hpp"
 #include "q4q8_common.hpp"
 
 namespace jjo {
 namespace {
-
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));           // 16-B aligned
-typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
-typedef uint32_t u32x2a4 __attribute__((ext_vector_type(2), aligned(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int BN = 128;          // weight rows per workgroup
 constexpr int BM = 128;          // tokens per workgroup
@@ -73,33 +64,6 @@ constexpr int kSmemBytes = kOffW + 2 * kWBufBytes;       // 77824
 constexpr int kXUnits = kXsBytes / 16;                   // 1152 16-byte units per stage
 constexpr int kXRuns = kXUnits / 64;                     // 18 wave-sized (1 KB) runs
 
-constexpr uint32_t kBiasBits = 0x4B400000u;              // 1.5 * 2^23
-
-// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] + [15:14],
-// expcnt[6:4] = 7, lgkmcnt[11:8] = 15).
-#define JJO_GEMM_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n)&15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
-constexpr float kBias = 12582912.0f;
-
-typedef __attribute__((address_space(3))) void lds_void;
-
-// Position of tile-local row r (0..31) in the epilogue scale layout: the 16 rows
-// a lane half owns in the 32x32 MFMA output (rows 8q + 4h + i) become contiguous.
-__device__ __forceinline__ int epi_perm(int r) {
-    const int q = r >> 3, h = (r >> 2) & 1, i = r & 3;
-    return h * 16 + q * 4 + i;
-}
-
-// Epilogue of one 32x32 int MFMA tile: acc += d_w * round(sumi * d_x / 8).
-__device__ __forceinline__ void epilogue(f32x16 &acc, const i32x16 &d, const uint32_t (&wv)[8], float dx8,
-                                         float nb8) {
-#pragma unroll
-    for (int v = 0; v < 16; ++v) {
-        const f16x2 pr = __builtin_bit_cast(f16x2, wv[v >> 1]);
-        const float dwv = (float)((v & 1) ? pr.y : pr.x);
-        const float t = fmaf(__int_as_float(d[v]), dx8, nb8);
-        acc[v] = fmaf(dwv, t, acc[v]);
-    }
-}
 
 template <bool kGrouped>
 __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
@@ -338,9 +302,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
                 float dx8[2], nb8[2];
     #pragma unroll
                 for (int ct = 0; ct < 2; ++ct) {
-                    // From the fp16 bits (low half): d_x/8 and -1.5*2^23*d_x/8.
-                    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(dx8[ct]) : "v"(hdr[ct][b]), "s"(0.125f));
-                    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(nb8[ct]) : "v"(hdr[ct][b]), "s"(-kBias * 0.125f));
+                    x_scales(hdr[ct][b], dx8[ct], nb8[ct]);
                 }
                 uint32_t wv[2][8];
     #pragma unroll

@@ -1,0 +1,253 @@
+// Q4_0 x Q8_1 GEMM on gfx950 int8 matrix cores, 64 x 64 workgroup tiles: the form
+// for batches too small to fill the chip with the 128 x 128 kernel's tiles.
+//
+// Same math and epilogue as that kernel (mfma_q4q8_tile.hpp; reference per-block
+// epilogue src/cuda/mm_q4_0_q8_1.cu:71-93, summed over K at :256-269).  What
+// changes is the tiling:
+//   * a workgroup owns 64 weight rows x 64 tokens; four waves in 2 x 2, each owning
+//     ONE 32 x 32 MFMA tile, so a workgroup streams half the weight rows and a wave
+//     holds a quarter of the accumulators (about half the VGPRs, so more waves fit
+//     on a SIMD);
+//   * K stages of 128 values (one Q8_1 superblock), weights staged through
+//     registers (one block per thread) with nibbles expanded to int8 in LDS, activations by
+//     LDS DMA; both double-buffered, one barrier per stage, 38 KB of LDS;
+//   * inside a stage the MFMA of block b+1 is issued before the epilogue of block b.
+// At M = 64..512 and N = 14336 this launches 224..1792 workgroups instead of
+// 112..448.
+#include <hip/hip_fp16.h>
+
+#include <type_traits>
+
+#include "mfma_q4q8_tile.hpp"
+#include "q4q8_common.hpp"
+
+namespace jjo {
+namespace {
+
+constexpr int SBN = 64;   // weight rows per workgroup
+constexpr int SBM = 64;   // tokens per workgroup
+constexpr int SKB = 4;    // 32-blocks per stage
+constexpr int kSThreads = 256;
+
+constexpr int kSXsBytes = SBM * kQ8BlockBytes;            // 9216 per stage: [SBM][144]
+constexpr int kSWqStride = SKB * 32 + 16;                 // 144: one row's 4 unpacked blocks + pad
+constexpr int kSWqBytes = SBN * kSWqStride;               // 9216
+constexpr int kSWdEpiBytes = SKB * SBN * 2;               // [SKB][SBN] fp16, rows permuted per 32
+constexpr int kSWdRowBytes = SBN * SKB * 2;               // [SBN][SKB] fp16
+constexpr int kSWBufBytes = kSWqBytes + kSWdEpiBytes + kSWdRowBytes;
+constexpr int kSOffW = 2 * kSXsBytes;
+constexpr int kSOffWdEpi = kSWqBytes;
+constexpr int kSOffWdRow = kSWqBytes + kSWdEpiBytes;
+constexpr int kSSmemBytes = kSOffW + 2 * kSWBufBytes;     // 38912
+constexpr int kSXRuns = kSXsBytes / 1024;                 // 9 wave-sized (1 KB) runs per stage
+
+__global__ __launch_bounds__(kSThreads) void gemm_q4_0_q8_1_mfma64_kernel(const uint8_t *__restrict__ w,
+                                                                         const uint8_t *__restrict__ xq,
+                                                                         float *__restrict__ y, int K, int N,
+                                                                         int M) {
+    extern __shared__ __align__(16) uint8_t smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn = wave >> 1;  // 32-row half of the workgroup tile
+    const int wm = wave & 1;   // 32-token half
+    const int l32 = lane & 31;
+    const int hh = lane >> 5;
+
+    const int n0 = blockIdx.x * SBN;
+    const int m0 = blockIdx.y * SBM;
+    const size_t row_bytes = (size_t)(K / kQK) * kQ4BlockBytes;
+    const int n_stages = K / (SKB * kQK);
+
+    // ---- weights: one 18-byte block per thread (row tid/4, block tid%4 of the stage) ----
+    // Block b of a stage starts 72c + 18b bytes into the row: 4-byte aligned for even b,
+    // 2 bytes past a dword for odd b.  Five aligned dwords cover it either way.
+    const int st_row = tid >> 2;
+    const int st_blk = tid & 3;
+    const bool st_odd = st_blk & 1;
+    const uint8_t *w_src =
+        w + (size_t)min(n0 + st_row, N - 1) * row_bytes + (size_t)((st_blk * kQ4BlockBytes) & ~3);
+    uint32_t wr0[5], wr1[5];
+    // Two vector-memory instructions per call (the explicit waits count on it).
+    auto load_w = [&](int c, uint32_t(&wst)[5]) {
+        const uint8_t *p = w_src + (size_t)c * (SKB * kQ4BlockBytes);
+        const u32x4a4 a = *reinterpret_cast<const u32x4a4 *>(p);
+        wst[0] = a.x; wst[1] = a.y; wst[2] = a.z; wst[3] = a.w;
+        wst[4] = *reinterpret_cast<const uint32_t *>(p + 16);
+    };
+    auto store_w = [&](int buf, const uint32_t(&wst)[5]) {
+        uint8_t *wq = smem + kSOffW + buf * kSWBufBytes;
+        uint32_t q[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) q[k] = st_odd ? wst[k + 1] : __builtin_amdgcn_alignbyte(wst[k + 1], wst[k], 2);
+        const uint32_t dbits = st_odd ? (wst[0] >> 16) : (wst[0] & 0xffffu);
+        u32x4 lo, hi;
+        lo.x = q[0] & 0x0f0f0f0fu; lo.y = q[1] & 0x0f0f0f0fu;
+        lo.z = q[2] & 0x0f0f0f0fu; lo.w = q[3] & 0x0f0f0f0fu;
+        hi.x = (q[0] >> 4) & 0x0f0f0f0fu; hi.y = (q[1] >> 4) & 0x0f0f0f0fu;
+        hi.z = (q[2] >> 4) & 0x0f0f0f0fu; hi.w = (q[3] >> 4) & 0x0f0f0f0fu;
+        uint8_t *dst = wq + st_row * kSWqStride + st_blk * 32;
+        *reinterpret_cast<u32x4 *>(dst) = lo;
+        *reinterpret_cast<u32x4 *>(dst + 16) = hi;
+        const unsigned short dh = (unsigned short)dbits;
+        reinterpret_cast<unsigned short *>(wq + kSOffWdEpi)[st_blk * SBN + (st_row & ~31) + epi_perm(st_row & 31)] = dh;
+        reinterpret_cast<unsigned short *>(wq + kSOffWdRow)[st_row * SKB + st_blk] = dh;
+    };
+
+    // ---- activations: runs r = wave, wave + 4, wave + 8 (< 9) of 1 KB by LDS DMA ----
+    // Units past the last valid token re-read unit 0; those tokens' (d, s) headers are
+    // zeroed once the tile has landed, so every product with them is zero.
+    const size_t x_stride = (size_t)M * kQ8BlockBytes;
+    const uint8_t *x_base = xq + (size_t)m0 * kQ8BlockBytes;
+    const int x_valid_tokens = min(SBM, M - m0);
+    const int x_valid_units = x_valid_tokens * (kQ8BlockBytes / 16);
+    uint32_t x_off[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int unit = min(wave + 4 * i, kSXRuns - 1) * 64 + lane;
+        x_off[i] = unit < x_valid_units ? unit * 16 : 0;
+    }
+    // Inline-asm DMA, as in the 128 x 128 kernel: the compiler's wait insertion would
+    // otherwise wait for every load in flight before the next LDS access.  Waited for
+    // explicitly below; the hardware counter counts them like any load.
+    auto load_x = [&](int c) {
+        const uint32_t xs = (uint32_t)(uintptr_t)(smem + (c & 1) * kSXsBytes);
+        const uint8_t *src = x_base + (size_t)c * x_stride;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const int run = wave + 4 * i;
+            if (run >= kSXRuns || run * 64 >= x_valid_units) continue;  // uniform per wave
+            const uint32_t m0v = __builtin_amdgcn_readfirstlane(xs + run * 1024);
+            asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src + x_off[i]), "{m0}"(m0v) : "memory");
+        }
+    };
+    auto zero_tail_headers = [&](int buf) {
+        if (x_valid_tokens < SBM) {  // uniform over the workgroup
+            if (tid >= x_valid_tokens && tid < SBM)
+                *reinterpret_cast<u32x4 *>(smem + buf * kSXsBytes + tid * kQ8BlockBytes) = u32x4{0u, 0u, 0u, 0u};
+            __syncthreads();
+        }
+    };
+
+    f32x16 acc;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
+    i32x16 bias;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) bias[v] = (int32_t)kBiasBits;
+    asm volatile("" : "+v"(bias));
+
+    // Pipeline as in the 128 x 128 kernel: X(c+1) and W(c+1), W(c+2) in flight while
+    // stage c is computed from buffers c & 1.
+    load_x(0);
+    load_w(0, wr0);
+    load_w(min(1, n_stages - 1), wr1);
+    JJO_GEMM_VMCNT(2);
+    store_w(0, wr0);
+    __syncthreads();
+    zero_tail_headers(0);
+    load_x(min(1, n_stages - 1));
+    load_w(min(2, n_stages - 1), wr0);
+
+    const int col = wm * 32 + l32;  // this lane's token in the tile
+    const int row = wn * 32 + l32;  // this lane's weight row for the A operand
+    auto stage = [&](int c, auto par_tag) {
+        constexpr int PAR = decltype(par_tag)::value;
+        uint32_t(&w_next)[5] = *[&]() { if constexpr (PAR) return &wr0; else return &wr1; }();
+        const uint8_t *wq = smem + kSOffW + (c & 1) * kSWBufBytes;
+        const uint8_t *xs = smem + (c & 1) * kSXsBytes;
+
+        const u32x4 h = *reinterpret_cast<const u32x4 *>(xs + col * kQ8BlockBytes);
+        const uint32_t hdr[4] = {h.x, h.y, h.z, h.w};
+        auto operands = [&](int b, i32x4 &aop, i32x4 &bop) {
+            aop = *reinterpret_cast<const i32x4 *>(wq + row * kSWqStride + b * 32 + 16 * hh);
+            bop = *reinterpret_cast<const i32x4 *>(xs + col * kQ8BlockBytes + 16 + 32 * b + 16 * hh);
+        };
+        auto scales = [&](int b, uint32_t(&wv)[8]) {
+            const _Float16 *wd_epi = reinterpret_cast<const _Float16 *>(wq + kSOffWdEpi);
+            const int rbase = wn * 32 + hh * 16;
+            const u32x4 w0 = *reinterpret_cast<const u32x4 *>(wd_epi + b * SBN + rbase);
+            const u32x4 w1 = *reinterpret_cast<const u32x4 *>(wd_epi + b * SBN + rbase + 8);
+            wv[0] = w0.x; wv[1] = w0.y; wv[2] = w0.z; wv[3] = w0.w;
+            wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
+        };
+        i32x4 a0, b0, a1, b1;
+        operands(0, a0, b0);
+        i32x16 d_prev = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, bias, 0, 0, 0);
+#pragma unroll
+        for (int b = 0; b < SKB; ++b) {
+            i32x16 d_next;
+            if (b + 1 < SKB) {
+                operands(b + 1, a1, b1);
+                d_next = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, bias, 0, 0, 0);
+            }
+            uint32_t wv[8];
+            scales(b, wv);
+            float dx8, nb8;
+            x_scales(hdr[b], dx8, nb8);
+            epilogue(acc, d_prev, wv, dx8, nb8);
+            if (b + 1 < SKB) d_prev = d_next;
+        }
+        // sum_b d_w * (-s_x) over the stage's 4 blocks on the f16 MFMA (K = 8: the
+        // lanes of the upper K half contribute zeros).
+        {
+            const f16x4 aop =
+                *reinterpret_cast<const f16x4 *>(wq + kSOffWdRow + (size_t)row * SKB * sizeof(_Float16));
+            uint32_t lo = ((hdr[0] >> 16) | (hdr[1] & 0xffff0000u)) ^ 0x80008000u;
+            uint32_t hi = ((hdr[2] >> 16) | (hdr[3] & 0xffff0000u)) ^ 0x80008000u;
+            // Zero B (not A) in the upper K half: an infinite s_x must not meet 0.
+            if (hh) { lo = 0u; hi = 0u; }
+            const u32x2 pk = {lo, hi};
+            acc = __builtin_amdgcn_mfma_f32_32x32x8f16(aop, __builtin_bit_cast(f16x4, pk), acc, 0, 0, 0);
+        }
+        // Unconditional (clamped past the last stage) so every path issues the same
+        // loads and the waits stay exact.
+        JJO_GEMM_VMCNT(2);  // all but W(c+2): X(c+1) and W(c+1) have landed
+        store_w((c + 1) & 1, w_next);
+        __syncthreads();
+        zero_tail_headers((c + 1) & 1);
+        load_x(min(c + 2, n_stages - 1));
+        load_w(min(c + 3, n_stages - 1), w_next);
+    };
+    int c = 0;
+    for (; c + 1 < n_stages; c += 2) {
+        stage(c, std::integral_constant<int, 0>{});
+        stage(c + 1, std::integral_constant<int, 1>{});
+    }
+    if (c < n_stages) stage(c, std::integral_constant<int, 0>{});
+    JJO_GEMM_VMCNT(0);
+
+    // ---- store: y[m][n] = 8 * acc ----
+    const int m = m0 + col;
+    if (m < M) {
+        float *yrow = y + (size_t)m * N;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int n = n0 + wn * 32 + 8 * q + 4 * hh;
+            const float v0 = 8.0f * acc[4 * q + 0], v1 = 8.0f * acc[4 * q + 1];
+            const float v2 = 8.0f * acc[4 * q + 2], v3 = 8.0f * acc[4 * q + 3];
+            if (n + 3 < N && (N & 3) == 0) {
+                *reinterpret_cast<float4 *>(yrow + n) = make_float4(v0, v1, v2, v3);
+            } else {
+                if (n + 0 < N) yrow[n + 0] = v0;
+                if (n + 1 < N) yrow[n + 1] = v1;
+                if (n + 2 < N) yrow[n + 2] = v2;
+                if (n + 3 < N) yrow[n + 3] = v3;
+            }
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_gemm_mfma64(const void *w, const void *xq, float *y, int K, int N, int M, hipStream_t stream) {
+    hipError_t e = ensure_dynamic_lds((const void *)gemm_q4_0_q8_1_mfma64_kernel, kSSmemBytes);
+    if (e != hipSuccess) return e;
+    const dim3 grid((N + SBN - 1) / SBN, (M + SBM - 1) / SBM);
+    hipLaunchKernelGGL(gemm_q4_0_q8_1_mfma64_kernel, grid, dim3(kSThreads), kSSmemBytes, stream,
+                       (const uint8_t *)w, (const uint8_t *)xq, y, K, N, M);
+    return hipGetLastError();
+}
+
+}  // namespace jjo

@@ -50,6 +50,8 @@ hipError_t launch_gemm_skinny(const void *w, const void *xq, float *y, int K, in
 bool gemm_skinny_persist_supported(const void *w, const void *xq, int K, int M);
 hipError_t launch_gemm_skinny_persist(const void *w, const void *xq, float *y, int K, int N, int M,
                                       hipStream_t stream);
+hipError_t launch_gemm_mfma64(const void *w, const void *xq, float *y, int K, int N, int M,
+                              hipStream_t stream);
 hipError_t launch_gemm_mfma(const void *w, const void *xq, float *y, int K, int N, int M,
                             hipStream_t stream);
 hipError_t launch_gemm_mfma_grouped(const void *w, const void *xq, const int32_t *expert_offsets,
