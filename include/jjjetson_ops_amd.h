@@ -120,6 +120,7 @@ int mat_mul_q4_0_q8_1_f32_device(const void *d_w_q4_0, const float *d_x, void *d
 #define JJO_ALGO_SKINNY 3    /* int8 MFMA 16x16 tiles streaming weights per wave, batch <= 32 */
 #define JJO_ALGO_SKINNY_LDS 4 /* int8 MFMA 16x16 tiles, activation resident in LDS, batch <= 16 */
 #define JJO_ALGO_MFMA64 5     /* int8 MFMA GEMM with 64x64 workgroup tiles, any batch */
+#define JJO_ALGO_MFMA32 6     /* int8 MFMA GEMM with 32-row x 64-token workgroup tiles, any batch */
 
 /*
  * As mat_mul_q4_0_q8_1_device with an explicit kernel choice.  Has no

@@ -24,6 +24,7 @@ ALGO_MFMA = 2
 ALGO_SKINNY = 3
 ALGO_SKINNY_LDS = 4
 ALGO_MFMA64 = 5
+ALGO_MFMA32 = 6
 
 QK = 32
 QSUPER = 128

@@ -197,9 +197,9 @@ int run_mm(const void *w, const void *xq, float *y, int K, int N, int M, int alg
                              "weights (batch=%d K=%d)", M, K);
         e = launch_gemm_skinny_persist(w, xq, y, K, N, M, s);
         if (e != hipSuccess) return hip_fail(e, "gemm_skinny_persist launch");
-    } else if (algo == JJO_ALGO_MFMA64) {
+    } else if (algo == JJO_ALGO_MFMA64 || algo == JJO_ALGO_MFMA32) {
         if ((M + 63) / 64 > 65535) return set_error(JJO_ERR_INVALID_ARG, "batch too large");
-        e = launch_gemm_mfma64(w, xq, y, K, N, M, s);
+        e = launch_gemm_mfma64(w, xq, y, K, N, M, s, algo == JJO_ALGO_MFMA32 ? 32 : 64);
         if (e != hipSuccess) return hip_fail(e, "gemm_q4_0_q8_1_mfma64 launch");
     } else if (algo == JJO_ALGO_MFMA) {
         if ((M + 127) / 128 > 65535) return set_error(JJO_ERR_INVALID_ARG, "batch too large");

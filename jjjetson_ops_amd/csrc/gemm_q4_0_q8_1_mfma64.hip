@@ -24,34 +24,51 @@
 namespace jjo {
 namespace {
 
-constexpr int SBN = 64;   // weight rows per workgroup
 constexpr int SBM = 64;   // tokens per workgroup
 constexpr int SKB = 4;    // 32-blocks per stage
 constexpr int kSThreads = 256;
 
 constexpr int kSXsBytes = SBM * kQ8BlockBytes;            // 9216 per stage: [SBM][144]
 constexpr int kSWqStride = SKB * 32 + 16;                 // 144: one row's 4 unpacked blocks + pad
-constexpr int kSWqBytes = SBN * kSWqStride;               // 9216
-constexpr int kSWdEpiBytes = SKB * SBN * 2;               // [SKB][SBN] fp16, rows permuted per 32
-constexpr int kSWdRowBytes = SBN * SKB * 2;               // [SBN][SKB] fp16
-constexpr int kSWBufBytes = kSWqBytes + kSWdEpiBytes + kSWdRowBytes;
-constexpr int kSOffW = 2 * kSXsBytes;
-constexpr int kSOffWdEpi = kSWqBytes;
-constexpr int kSOffWdRow = kSWqBytes + kSWdEpiBytes;
-constexpr int kSSmemBytes = kSOffW + 2 * kSWBufBytes;     // 38912
 constexpr int kSXRuns = kSXsBytes / 1024;                 // 9 wave-sized (1 KB) runs per stage
 
+// LDS layout for TR weight rows per workgroup (64, or 32).
+template <int TR>
+struct SmallTile {
+    static constexpr int kWqBytes = TR * kSWqStride;
+    static constexpr int kWdEpiBytes = SKB * TR * 2;      // [SKB][TR] fp16, rows permuted per 32
+    static constexpr int kWdRowBytes = TR * SKB * 2;      // [TR][SKB] fp16
+    static constexpr int kWBufBytes = kWqBytes + kWdEpiBytes + kWdRowBytes;
+    static constexpr int kOffW = 2 * kSXsBytes;
+    static constexpr int kOffWdEpi = kWqBytes;
+    static constexpr int kOffWdRow = kWqBytes + kWdEpiBytes;
+    static constexpr int kSmemBytes = kOffW + 2 * kWBufBytes;  // 38912 (TR = 64), 28672 (TR = 32)
+    // K split between wave pairs: with 32 rows the four waves are 2 token halves x
+    // 2 halves of each stage's blocks, joined at the end in a fixed order.
+    static constexpr int KS = TR == 64 ? 1 : 2;
+};
+
+template <int TR>
 __global__ __launch_bounds__(kSThreads) void gemm_q4_0_q8_1_mfma64_kernel(const uint8_t *__restrict__ w,
                                                                          const uint8_t *__restrict__ xq,
                                                                          float *__restrict__ y, int K, int N,
                                                                          int M) {
     extern __shared__ __align__(16) uint8_t smem[];
+    using L = SmallTile<TR>;
+    constexpr int SBN = TR;
+    constexpr int kSWBufBytes = L::kWBufBytes;
+    constexpr int kSOffW = L::kOffW;
+    constexpr int kSOffWdEpi = L::kOffWdEpi;
+    constexpr int kSOffWdRow = L::kOffWdRow;
+    constexpr int KS = L::KS;
+    constexpr int kBlocksPerWave = SKB / KS;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wn = wave >> 1;  // 32-row half of the workgroup tile
-    const int wm = wave & 1;   // 32-token half
+    const int wm = wave & 1;                    // 32-token half
+    const int wn = KS == 1 ? wave >> 1 : 0;     // 32-row half of the workgroup tile
+    const int kh = KS == 1 ? 0 : wave >> 1;     // half of each stage's blocks
     const int l32 = lane & 31;
     const int hh = lane >> 5;
 
@@ -62,8 +79,11 @@ __global__ __launch_bounds__(kSThreads) void gemm_q4_0_q8_1_mfma64_kernel(const 
 
     // ---- weights: one 18-byte block per thread (row tid/4, block tid%4 of the stage) ----
     // Block b of a stage starts 72c + 18b bytes into the row: 4-byte aligned for even b,
-    // 2 bytes past a dword for odd b.  Five aligned dwords cover it either way.
-    const int st_row = tid >> 2;
+    // 2 bytes past a dword for odd b.  Five aligned dwords cover it either way.  With
+    // 32 rows the upper 128 threads repeat the loads of the lower ones (so every wave
+    // issues the same loads and the explicit waits hold) and store nothing.
+    const int st_row = (tid >> 2) & (TR - 1);
+    const bool st_store = TR == 64 || tid < 4 * TR;
     const int st_blk = tid & 3;
     const bool st_odd = st_blk & 1;
     const uint8_t *w_src =
@@ -77,6 +97,7 @@ __global__ __launch_bounds__(kSThreads) void gemm_q4_0_q8_1_mfma64_kernel(const 
         wst[4] = *reinterpret_cast<const uint32_t *>(p + 16);
     };
     auto store_w = [&](int buf, const uint32_t(&wst)[5]) {
+        if (!st_store) return;
         uint8_t *wq = smem + kSOffW + buf * kSWBufBytes;
         uint32_t q[4];
 #pragma unroll
@@ -172,26 +193,27 @@ __global__ __launch_bounds__(kSThreads) void gemm_q4_0_q8_1_mfma64_kernel(const 
             wv[0] = w0.x; wv[1] = w0.y; wv[2] = w0.z; wv[3] = w0.w;
             wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
         };
+        const int bb = kh * kBlocksPerWave;  // this wave's first block of the stage
         i32x4 a0, b0, a1, b1;
-        operands(0, a0, b0);
+        operands(bb, a0, b0);
         i32x16 d_prev = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, b0, bias, 0, 0, 0);
 #pragma unroll
-        for (int b = 0; b < SKB; ++b) {
+        for (int j = 0; j < kBlocksPerWave; ++j) {
             i32x16 d_next;
-            if (b + 1 < SKB) {
-                operands(b + 1, a1, b1);
+            if (j + 1 < kBlocksPerWave) {
+                operands(bb + j + 1, a1, b1);
                 d_next = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, bias, 0, 0, 0);
             }
             uint32_t wv[8];
-            scales(b, wv);
+            scales(bb + j, wv);
             float dx8, nb8;
-            x_scales(hdr[b], dx8, nb8);
+            x_scales(hdr[bb + j], dx8, nb8);
             epilogue(acc, d_prev, wv, dx8, nb8);
-            if (b + 1 < SKB) d_prev = d_next;
+            if (j + 1 < kBlocksPerWave) d_prev = d_next;
         }
         // sum_b d_w * (-s_x) over the stage's 4 blocks on the f16 MFMA (K = 8: the
-        // lanes of the upper K half contribute zeros).
-        {
+        // lanes of the upper K half contribute zeros), by the waves of the first half.
+        if (kh == 0) {
             const f16x4 aop =
                 *reinterpret_cast<const f16x4 *>(wq + kSOffWdRow + (size_t)row * SKB * sizeof(_Float16));
             uint32_t lo = ((hdr[0] >> 16) | (hdr[1] & 0xffff0000u)) ^ 0x80008000u;
@@ -218,6 +240,22 @@ __global__ __launch_bounds__(kSThreads) void gemm_q4_0_q8_1_mfma64_kernel(const 
     if (c < n_stages) stage(c, std::integral_constant<int, 0>{});
     JJO_GEMM_VMCNT(0);
 
+    if constexpr (KS == 2) {
+        __syncthreads();  // every wave's last (clamped) activation DMA has landed
+        // Join the two block halves: the second half's waves hand their accumulators
+        // over through LDS (the activation buffers, free after the last barrier) and
+        // the first half adds them, always in this order.
+        float *part = reinterpret_cast<float *>(smem) + (size_t)wm * 16 * 64;
+        if (kh == 1) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) part[v * 64 + lane] = acc[v];
+        }
+        __syncthreads();
+        if (kh == 1) return;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[v] += part[v * 64 + lane];
+    }
+
     // ---- store: y[m][n] = 8 * acc ----
     const int m = m0 + col;
     if (m < M) {
@@ -239,15 +277,23 @@ __global__ __launch_bounds__(kSThreads) void gemm_q4_0_q8_1_mfma64_kernel(const 
     }
 }
 
+template <int TR>
+hipError_t launch_small(const void *w, const void *xq, float *y, int K, int N, int M, hipStream_t stream) {
+    constexpr int smem = SmallTile<TR>::kSmemBytes;
+    hipError_t e = ensure_dynamic_lds((const void *)gemm_q4_0_q8_1_mfma64_kernel<TR>, smem);
+    if (e != hipSuccess) return e;
+    const dim3 grid((N + TR - 1) / TR, (M + SBM - 1) / SBM);
+    hipLaunchKernelGGL(gemm_q4_0_q8_1_mfma64_kernel<TR>, grid, dim3(kSThreads), smem, stream, (const uint8_t *)w,
+                       (const uint8_t *)xq, y, K, N, M);
+    return hipGetLastError();
+}
+
 }  // namespace
 
-hipError_t launch_gemm_mfma64(const void *w, const void *xq, float *y, int K, int N, int M, hipStream_t stream) {
-    hipError_t e = ensure_dynamic_lds((const void *)gemm_q4_0_q8_1_mfma64_kernel, kSSmemBytes);
-    if (e != hipSuccess) return e;
-    const dim3 grid((N + SBN - 1) / SBN, (M + SBM - 1) / SBM);
-    hipLaunchKernelGGL(gemm_q4_0_q8_1_mfma64_kernel, grid, dim3(kSThreads), kSSmemBytes, stream,
-                       (const uint8_t *)w, (const uint8_t *)xq, y, K, N, M);
-    return hipGetLastError();
+hipError_t launch_gemm_mfma64(const void *w, const void *xq, float *y, int K, int N, int M, hipStream_t stream,
+                              int tile_rows) {
+    return tile_rows == 32 ? launch_small<32>(w, xq, y, K, N, M, stream)
+                           : launch_small<64>(w, xq, y, K, N, M, stream);
 }
 
 }  // namespace jjo

@@ -50,8 +50,9 @@ hipError_t launch_gemm_skinny(const void *w, const void *xq, float *y, int K, in
 bool gemm_skinny_persist_supported(const void *w, const void *xq, int K, int M);
 hipError_t launch_gemm_skinny_persist(const void *w, const void *xq, float *y, int K, int N, int M,
                                       hipStream_t stream);
+// tile_rows: 64, or 32 (the stage's blocks split between wave pairs).
 hipError_t launch_gemm_mfma64(const void *w, const void *xq, float *y, int K, int N, int M,
-                              hipStream_t stream);
+                              hipStream_t stream, int tile_rows);
 hipError_t launch_gemm_mfma(const void *w, const void *xq, float *y, int K, int N, int M,
                             hipStream_t stream);
 hipError_t launch_gemm_mfma_grouped(const void *w, const void *xq, const int32_t *expert_offsets,

@@ -146,7 +146,7 @@ def test_gemv(K, N, M, dev):
     (4096, 256, 128), (4096, 300, 130), (256, 128, 1), (640, 200, 16), (11008, 128, 64), (384, 64, 257),
     (1024, 70, 33), (512, 4100, 96),
 ])
-@pytest.mark.parametrize("algo", [capi.ALGO_MFMA, capi.ALGO_MFMA64])
+@pytest.mark.parametrize("algo", [capi.ALGO_MFMA, capi.ALGO_MFMA64, capi.ALGO_MFMA32])
 def test_gemm_mfma(K, N, M, algo, dev):
     note(f"gemm mfma algo={algo} K={K} N={N} M={M}")
     w = make_w(N, K, 3 * N + K)
@@ -308,7 +308,7 @@ def test_infinite_block_sum_gives_inf_like_reference(M, dev):
     xq = c_oracle.quantize_q8_1(x, [K, M])
     exp = c_oracle.matmul(w, xq, K, N, M)
     assert np.all(np.isinf(exp[1]))
-    algos = [capi.ALGO_MFMA, capi.ALGO_MFMA64] + ([capi.ALGO_GEMV] if M <= 8 else []) + ([capi.ALGO_SKINNY] if M <= 32 else [])
+    algos = [capi.ALGO_MFMA, capi.ALGO_MFMA64, capi.ALGO_MFMA32] + ([capi.ALGO_GEMV] if M <= 8 else []) + ([capi.ALGO_SKINNY] if M <= 32 else [])
     algos += [capi.ALGO_SKINNY_LDS] if M <= 16 else []
     for algo in algos:
         got = run_mm(w, xq, K, N, M, algo, dev)
