@@ -169,7 +169,10 @@ int run_mm(const void *w, const void *xq, float *y, int K, int N, int M, int alg
         // that the 64 x 64 kernel runs four times as many workgroups and is up to 2x
         // faster (K=4096: N=14336 up to M=384, N=4096 up to M=1024).
         else if (2 * (int64_t)((N + 127) / 128) * ((M + 127) / 128) < 3 * (int64_t)device_cus())
-            algo = JJO_ALGO_MFMA64;
+            // Down to 1.5 workgroups of 64 x 64 per CU, 32-row tiles (twice the
+            // workgroups, each wave half of a stage's blocks) are 7-20% faster still.
+            algo = 2 * (int64_t)((N + 63) / 64) * ((M + 63) / 64) <= 3 * (int64_t)device_cus() ? JJO_ALGO_MFMA32
+                                                                                            : JJO_ALGO_MFMA64;
         else
             algo = JJO_ALGO_MFMA;
     }
