@@ -373,6 +373,8 @@ def main():
         ("m16_k4096_n14336", 16, 4096, 14336, 2, args.steps),
         ("prefill_m2048_k4096_n4096", 2048, 4096, 4096, 3, max(20, args.steps // 4)),
         ("prefill_m2048_k4096_n14336", 2048, 4096, 14336, 3, max(20, args.steps // 4)),
+        # Not a BASELINE.json config: a short prompt's prefill (small-tile GEMM range).
+        ("prefill_m128_k4096_n14336", 128, 4096, 14336, 3, max(20, args.steps // 4)),
     ]
     if args.only:
         if args.only == "moe_grouped_e8_top2_t512":
