@@ -1,13 +1,13 @@
 """Benchmark of the gfx950 Q4_0 x Q8_1 path (one JSON line on stdout).
 
-Headline workload (first call): decode GEMV at M=1,
+Headline workload (the decode GEMV, first of its two calls): M=1,
 K=4096 -> N=11008.  One step = quantize the fp32 activation to Q8_1 on the
 device + the Q4_0 x Q8_1 GEMV, exactly what a decode layer does per linear.
 ``value`` is effective weight GB/s of the whole step (weight bytes / step
 time).  Weight buffers rotate over > 512 MB so the 256 MB MALL cannot serve
 them.  Timed steps are captured in one HIP graph and replayed, bracketed by
 HIP events on the launch stream.  ``roofline`` is the GEMV kernel alone (a
-graph of back-to-back GEMV launches).  The other BASELINE configs are measured
+graph of back-to-back GEMV launches).  The other configurations are measured
 the same way and reported under ``configs``.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick] [--no-cpu]
@@ -139,7 +139,7 @@ def time_linear(name, M, K, N, seed, dev, steps, warmup, outliers=True):
 
 
 def time_moe(dev, steps, warmup):
-    """8 experts, top-2 of 512 tokens, K=4096 -> N=14336, one launch."""
+    """MoE expert GEMM: 8 experts, top-2 of 512 tokens, K=4096 -> N=14336, one launch."""
     import torch
     from jjjetson_ops_amd import capi
 
@@ -373,7 +373,7 @@ def main():
         ("m16_k4096_n14336", 16, 4096, 14336, 2, args.steps),
         ("prefill_m2048_k4096_n4096", 2048, 4096, 4096, 3, max(20, args.steps // 4)),
         ("prefill_m2048_k4096_n14336", 2048, 4096, 14336, 3, max(20, args.steps // 4)),
-        # Not a BASELINE.json config: a short prompt's prefill (small-tile GEMM range).
+        # A short prompt's prefill (the small-tile GEMM range), beside the headline configs.
         ("prefill_m128_k4096_n14336", 128, 4096, 14336, 3, max(20, args.steps // 4)),
     ]
     if args.only:

@@ -144,7 +144,7 @@ def test_gemv(K, N, M, dev):
 
 @pytest.mark.parametrize("K,N,M", [
     (4096, 256, 128), (4096, 300, 130), (256, 128, 1), (640, 200, 16), (11008, 128, 64), (384, 64, 257),
-    (1024, 70, 33), (512, 4100, 96),
+    (1024, 70, 33), (512, 4100, 96), (128, 96, 70), (128, 5, 40),
 ])
 @pytest.mark.parametrize("algo", [capi.ALGO_MFMA, capi.ALGO_MFMA64, capi.ALGO_MFMA32])
 def test_gemm_mfma(K, N, M, algo, dev):
@@ -183,7 +183,7 @@ def test_gemm_skinny_lds(K, N, M, dev):
 
 
 def test_gemm_skinny_lds_full_size(dev):
-    """BASELINE config 3 at M=16 (K=4096, N=14336: four tiles per workgroup)."""
+    """Small-batch decode at M=16 (K=4096, N=14336: four tiles per workgroup)."""
     K, N, M = 4096, 14336, 16
     note(f"gemm skinny lds full size K={K} N={N} M={M}")
     w = make_w(N, K, 2)

@@ -309,7 +309,7 @@ def test_matmul_closed_forms():
 
 @pytest.mark.parametrize("K,N,M", [(4096, 64, 1), (512, 40, 5)])
 def test_matmul_matches_dequantized_dense(K, N, M):
-    """y ~ dequant(W) . x within the quantisation error (BASELINE config 1 sanity)."""
+    """y ~ dequant(W) . x within the quantisation error (the plumbing case's sanity check)."""
     wf, w, x, xq = _rand_case(K, N, M, 5)
     y = c_oracle.matmul(w, xq, K, N, M)
     wdq = q4_0.dequantize_q4_0_np(w, N, K).astype(np.float64)
