@@ -23,6 +23,19 @@ def test_header_declares_what_capi_binds():
     assert declared_functions() == sorted(capi.EXPORTED_SYMBOLS)
 
 
+def test_header_constants_match_capi():
+    """Every JJO_* status, algorithm and weight-dtype constant of the header has the
+    same value in capi.py (JJO_ALGO_X -> ALGO_X, JJO_WEIGHT_DTYPE_X -> WEIGHT_DTYPE_X,
+    status codes under their own names)."""
+    consts = dict(re.findall(r"^#define\s+JJO_([A-Z0-9_]+)\s+(-?\d+)", HEADER.read_text(), flags=re.M))
+    assert any(k.startswith("ALGO_") for k in consts)
+    for name, value in consts.items():
+        if name.startswith(("ALGO_", "WEIGHT_DTYPE_")):
+            assert getattr(capi, name) == int(value), name
+        elif name.startswith("ERR_") or name == "OK":
+            assert getattr(capi, "JJO_" + name) == int(value), name
+
+
 def test_library_exports_every_declared_symbol():
     L = ctypes.CDLL(str(capi.LIB_PATH))
     for name in declared_functions():
