@@ -113,6 +113,53 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (r0 + r1) + (r2 + r3);
 }
 
+// NV independent 64-lane sums at once (NV a power of two, <= 16).  Transposed
+// butterfly: in round r (distance 32 >> r) each lane keeps one of every pair of its
+// values, adds its partner's copy of it and sends the other, so the values per lane
+// halve while the lanes per partial double.  After log2(NV) rounds every lane holds
+// one partial, for value sum_r bit(5 - r of lane) << r; a plain reduction over the
+// remaining 64 / NV lanes that share it finishes the sum.  Returns the lane's sum.
+template <int NV>
+__device__ __forceinline__ float multi_sum(float (&v)[NV], int lane) {
+    static_assert(NV == 1 || NV == 2 || NV == 4 || NV == 8 || NV == 16, "NV");
+    constexpr int R = NV == 1 ? 0 : NV == 2 ? 1 : NV == 4 ? 2 : NV == 8 ? 3 : 4;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int dist = 32 >> r;
+        const bool bit = lane & dist;
+#pragma unroll
+        for (int j = 0; j < (NV >> r) / 2; ++j) {
+            const float keep = bit ? v[2 * j + 1] : v[2 * j];
+            const float send = bit ? v[2 * j] : v[2 * j + 1];
+            v[j] = keep + __shfl_xor(send, dist);
+        }
+    }
+    constexpr int G = 64 >> R;  // lanes that share a value
+    float t = v[0];
+    if constexpr (G >= 2) t += dpp<0xB1>(t);   // quad_perm [1,0,3,2]
+    if constexpr (G >= 4) t += dpp<0x4E>(t);   // quad_perm [2,3,0,1]
+    if constexpr (G == 8) t += dpp<0x141>(t);  // row_half_mirror: the other quad of 8
+    if constexpr (G >= 16) {
+        t += dpp<0x124>(t);  // row_ror:4
+        t += dpp<0x128>(t);  // row_ror:8
+    }
+    if constexpr (G >= 32) t += __shfl_xor(t, 16);
+    if constexpr (G == 64) t += __shfl_xor(t, 32);
+    return t;
+}
+
+// Value index whose sum multi_sum<NV> leaves in `lane`.
+template <int NV>
+__device__ __forceinline__ int multi_sum_index(int lane) {
+    constexpr int R = NV == 1 ? 0 : NV == 2 ? 1 : NV == 4 ? 2 : NV == 8 ? 3 : 4;
+    int idx = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) idx |= ((lane >> (5 - r)) & 1) << r;
+    return idx;
+}
+
+constexpr int pow2_at_least(int n) { return n <= 1 ? 1 : 2 * pow2_at_least((n + 1) / 2); }
+
 // Write one block's planes and constants into its half of the pair record.
 __device__ __forceinline__ void put_block(uint8_t *rec, int half, const uint32_t hi[4], const uint32_t lo[4],
                                           float dx, float c) {
@@ -362,13 +409,15 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
     }
 
     if constexpr (JS == 1) {
+        // All U * M sums of the wave in one transposed reduction.
+        constexpr int NV = pow2_at_least(U * M);
+        float v[NV];
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-                const float s = wave_sum(acc[u][m]);
-                if (lane == ((u * M + m) & 63) && r0 + u < N) y[(size_t)m * N + r0 + u] = s;
-            }
+        for (int i = 0; i < NV; ++i) v[i] = i < U * M ? acc[i / M][i % M] : 0.0f;
+        const float s = multi_sum<NV>(v, lane);
+        const int idx = multi_sum_index<NV>(lane);
+        const int u = idx / M, m = idx % M;
+        if ((lane & (64 / NV - 1)) == 0 && idx < U * M && r0 + u < N) y[(size_t)m * N + r0 + u] = s;
     } else {
 #pragma unroll
         for (int u = 0; u < U; ++u)
