@@ -24,7 +24,8 @@
 //     with the reference quantizer's arithmetic (exact sum tree, IEEE divides,
 //     roundf), optionally writing the Q8_1 bytes too.  One 80-byte LDS record
 //     per (token, block pair): conflict-free ds_read_b128 for consecutive lanes.
-//   * Lane partials: DPP quad/row rotations and four v_readlane; the JS
+//   * Lane partials: one transposed butterfly for all of a wave's row x token
+//     sums (ds_bpermute rounds, then DPP within the lanes that share a sum); the JS
 //     K-slices of a row group (JS waves of one workgroup) are added in LDS in
 //     slice order.
 #include <hip/hip_fp16.h>
@@ -98,19 +99,6 @@ __device__ __forceinline__ int32_t nib_sum128(const uint32_t w[4]) {
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-
-// Sum over the 64 lanes, returned as a wave-uniform value.
-__device__ __forceinline__ float wave_sum(float v) {
-    v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
-    v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
-    v += dpp<0x124>(v);  // row_ror:4
-    v += dpp<0x128>(v);  // row_ror:8  -> every lane holds its 16-lane row sum
-    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
-    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
-    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
-    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
-    return (r0 + r1) + (r2 + r3);
 }
 
 // NV independent 64-lane sums at once (NV a power of two, <= 16).  Transposed
@@ -408,24 +396,20 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
         }
     }
 
+    // All U * M sums of the wave in one transposed reduction; lane `owner` of each
+    // group that shares a value holds its sum.
+    constexpr int NV = pow2_at_least(U * M);
+    float v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] = i < U * M ? acc[i / M][i % M] : 0.0f;
+    const float s = multi_sum<NV>(v, lane);
+    const int idx = multi_sum_index<NV>(lane);
+    const int u = idx / M, m = idx % M;
+    const bool owner = (lane & (64 / NV - 1)) == 0 && idx < U * M;
     if constexpr (JS == 1) {
-        // All U * M sums of the wave in one transposed reduction.
-        constexpr int NV = pow2_at_least(U * M);
-        float v[NV];
-#pragma unroll
-        for (int i = 0; i < NV; ++i) v[i] = i < U * M ? acc[i / M][i % M] : 0.0f;
-        const float s = multi_sum<NV>(v, lane);
-        const int idx = multi_sum_index<NV>(lane);
-        const int u = idx / M, m = idx % M;
-        if ((lane & (64 / NV - 1)) == 0 && idx < U * M && r0 + u < N) y[(size_t)m * N + r0 + u] = s;
+        if (owner && r0 + u < N) y[(size_t)m * N + r0 + u] = s;
     } else {
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-                const float s = wave_sum(acc[u][m]);
-                if (lane == 0) part[((rg * U + u) * M + m) * JS + js] = s;
-            }
+        if (owner) part[((rg * U + u) * M + m) * JS + js] = s;
         __syncthreads();
         if (js == 0) {
 #pragma unroll
