@@ -259,11 +259,13 @@ def test_quantizers_round_the_product_first(K, N, dev):
     assert np.array_equal(xq.cpu().numpy(), xq_ref)
 
 
-@pytest.mark.parametrize("M", [2, 5])
-def test_f32_entry_batched(M, dev):
+@pytest.mark.parametrize("K,N,M", [(512, 100, 2), (512, 100, 5), (4096, 257, 2), (4096, 257, 3), (4096, 300, 4),
+                                   (11008, 64, 2), (11008, 64, 3), (128, 7, 4)])
+def test_f32_entry_batched(K, N, M, dev):
+    """fp32 activation entry at batch > 1: a quantizer launch + matmul; the Q8_1
+    workspace is bit-exact."""
     import torch
-    K, N = 512, 100
-    note(f"f32 entry batched M={M}")
+    note(f"f32 entry batched K={K} N={N} M={M}")
     w = make_w(N, K, 77)
     x = make_x(K, M, 78)
     xq_ref = c_oracle.quantize_q8_1(x, [K, M])
