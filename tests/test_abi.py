@@ -1,5 +1,10 @@
 """The C-ABI library and the pybind11 modules load, export every declared
 symbol, and validate arguments — all without a GPU (no compute calls)."""
+if __name__ == "__main__":  # `python tests/<file>.py`, as the reference runs its tests
+    import sys as _sys
+
+    import pytest as _pytest
+    _sys.exit(_pytest.main([__file__, "-q"]))
 import ctypes
 import re
 from pathlib import Path

@@ -1,5 +1,10 @@
 """The C ABI from a plain C program (gcc, no C++ or Python in between): the
 header compiles as C and the Q4_0 weight entries work end to end (no GPU)."""
+if __name__ == "__main__":  # `python tests/<file>.py`, as the reference runs its tests
+    import sys as _sys
+
+    import pytest as _pytest
+    _sys.exit(_pytest.main([__file__, "-q"]))
 import shutil
 import subprocess
 from pathlib import Path

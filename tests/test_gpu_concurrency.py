@@ -1,5 +1,10 @@
 """Library calls from several host threads on separate HIP streams, in a fresh
 process so that their one-time per-kernel set-up also runs concurrently."""
+if __name__ == "__main__":  # `python tests/<file>.py`, as the reference runs its tests
+    import sys as _sys
+
+    import pytest as _pytest
+    _sys.exit(_pytest.main([__file__, "-q"]))
 import subprocess
 import sys
 from pathlib import Path

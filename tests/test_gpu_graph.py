@@ -2,6 +2,11 @@
 eager result bit for bit (no memset nodes, no hidden allocation, no state carried
 between calls).  Each graph is replayed several times with unrelated eager work and
 synchronisations in between."""
+if __name__ == "__main__":  # `python tests/<file>.py`, as the reference runs its tests
+    import sys as _sys
+
+    import pytest as _pytest
+    _sys.exit(_pytest.main([__file__, "-q"]))
 import sys
 
 import numpy as np

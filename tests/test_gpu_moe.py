@@ -13,6 +13,11 @@ Bars:
     SwiGLU output, which the fp32/fp64 difference of the gate/up sums can move by one
     Q8_1 step in rare elements).
 """
+if __name__ == "__main__":  # `python tests/<file>.py`, as the reference runs its tests
+    import sys as _sys
+
+    import pytest as _pytest
+    _sys.exit(_pytest.main([__file__, "-q"]))
 import sys
 
 import numpy as np

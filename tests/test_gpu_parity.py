@@ -5,6 +5,11 @@ Bars:
   * per-block int32 dot sums           : bit-exact
   * fp32 outputs                       : rtol 1e-3, atol 1e-4 against the fp64 oracle
 """
+if __name__ == "__main__":  # `python tests/<file>.py`, as the reference runs its tests
+    import sys as _sys
+
+    import pytest as _pytest
+    _sys.exit(_pytest.main([__file__, "-q"]))
 import sys
 
 import numpy as np

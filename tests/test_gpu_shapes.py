@@ -2,6 +2,11 @@
 AUTO, against the CPU oracle.  The shapes cover tails in all three dimensions
 (K in 128..1024, N in 1..300, M in 1..160).  Each kernel that accepts a shape also
 runs on a 4-byte-offset weight buffer, which is the layout's guaranteed alignment."""
+if __name__ == "__main__":  # `python tests/<file>.py`, as the reference runs its tests
+    import sys as _sys
+
+    import pytest as _pytest
+    _sys.exit(_pytest.main([__file__, "-q"]))
 import sys
 
 import numpy as np

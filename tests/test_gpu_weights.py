@@ -1,5 +1,10 @@
 """GPU: the device Q4_0 quantizer against the C oracle (bit-exact), and a Q4_0
 checkpoint written by the repacker feeding the GEMV."""
+if __name__ == "__main__":  # `python tests/<file>.py`, as the reference runs its tests
+    import sys as _sys
+
+    import pytest as _pytest
+    _sys.exit(_pytest.main([__file__, "-q"]))
 import sys
 
 import numpy as np

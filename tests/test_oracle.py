@@ -10,6 +10,11 @@ Each check is chosen so a plausible restatement mistake fails it:
   * nibble pairing (j, j+16) / unsigned nibbles           -> test_block_sums_bruteforce
   * epilogue sign / factor 8 / scale operands             -> test_matmul_closed_forms
 """
+if __name__ == "__main__":  # `python tests/<file>.py`, as the reference runs its tests
+    import sys as _sys
+
+    import pytest as _pytest
+    _sys.exit(_pytest.main([__file__, "-q"]))
 from fractions import Fraction
 
 import numpy as np

@@ -2,6 +2,11 @@
 place of roundf.  This checks, over every non-negative float32 below 2^23, that
 the two give the same integer (ties away from zero); the sign makes it symmetric.
 Pure NumPy, ~20 s."""
+if __name__ == "__main__":  # `python tests/<file>.py`, as the reference runs its tests
+    import sys as _sys
+
+    import pytest as _pytest
+    _sys.exit(_pytest.main([__file__, "-q"]))
 import numpy as np
 
 

@@ -1,6 +1,11 @@
 """On-disk Q4_0 weights, host side (no GPU): the host quantizer against the C
 oracle, closed-form round trips, the safetensors reader / writer against the stock
 `safetensors` package, the streaming repacker and its error paths."""
+if __name__ == "__main__":  # `python tests/<file>.py`, as the reference runs its tests
+    import sys as _sys
+
+    import pytest as _pytest
+    _sys.exit(_pytest.main([__file__, "-q"]))
 import json
 import struct
 
