@@ -149,6 +149,11 @@ int mat_mul_q4_0_q8_1_block_sums_device(const void *d_w_q4_0, const void *d_x_q8
  * routed activations, superblock-major over n_routes "tokens".  Expert e's
  * weight is d_w_q4_0 + e*nrows_out*(ncols_k/32)*18.  Route r's output row goes
  * to d_y[route_dst[r]*nrows_out ...] (route_dst may be NULL: identity).
+ * expert_offsets (device, E+1 entries) must be non-decreasing with
+ * expert_offsets[0] == 0 and expert_offsets[E] == n_routes; the kernel clamps
+ * every range to [0, n_routes], so a malformed table drops routes instead of
+ * reading or writing outside the buffers.  (n_routes+127)/128 + n_experts must
+ * not exceed 65535.
  */
 int mat_mul_q4_0_q8_1_grouped_device(const void *d_w_q4_0, const void *d_x_q8_1,
                                      const int32_t *d_expert_offsets, int n_experts,

@@ -150,6 +150,14 @@ int validate_mm(const void *w, const void *xq, const void *y, int K, int N, int 
     return JJO_OK;
 }
 
+// The grouped GEMM launches one workgroup row per possible token tile.
+int check_grouped_grid(int n_routes, int n_experts) {
+    if ((int64_t)(n_routes + 127) / 128 + n_experts > 65535)
+        return set_error(JJO_ERR_INVALID_ARG, "grouped matmul: %d routes over %d experts exceed one launch's tiles",
+                         n_routes, n_experts);
+    return JJO_OK;
+}
+
 int run_mm(const void *w, const void *xq, float *y, int K, int N, int M, int algo, hipStream_t s) {
     if (algo == JJO_ALGO_AUTO) {
         const bool gemv_ok = M <= kGemvMaxBatch && K <= kGemvMaxK && (int64_t)M * (K / 64) * 80 <= 150 * 1024;
@@ -381,6 +389,7 @@ int mat_mul_q4_0_q8_1_grouped_device(const void *d_w_q4_0, const void *d_x_q8_1,
     if (rc != JJO_OK) return rc;
     if (d_expert_offsets == nullptr || n_experts <= 0 || n_experts > 4096)
         return set_error(JJO_ERR_INVALID_ARG, "expert_offsets must be non-null and 1 <= n_experts <= 4096");
+    if ((rc = check_grouped_grid(n_routes, n_experts)) != JJO_OK) return rc;
     if ((rc = require_gfx950()) != JJO_OK) return rc;
     hipError_t e = launch_gemm_mfma_grouped(d_w_q4_0, d_x_q8_1, d_expert_offsets, n_experts, d_route_dst,
                                             d_y, ncols_k, nrows_out, n_routes, (hipStream_t)stream);
@@ -528,6 +537,9 @@ int check_moe_shape(int num_tokens, int hidden, int inter, int num_experts, int 
                          "(got top_k=%d num_experts=%d)", top_k, num_experts);
     if ((int64_t)num_tokens * top_k > 0x7fffffffLL / 4)
         return set_error(JJO_ERR_INVALID_ARG, "moe: too many routes");
+    if (num_tokens > 65535 || ((int64_t)num_tokens * top_k + 127) / 128 + num_experts > 65535)
+        return set_error(JJO_ERR_INVALID_ARG, "moe: num_tokens=%d with top_k=%d exceeds one launch's grid",
+                         num_tokens, top_k);
     return JJO_OK;
 }
 
@@ -628,6 +640,7 @@ int moe_q4_0_gate_up_device(void *stream, const void *w_gate, const void *w_up, 
         return set_error(JJO_ERR_INVALID_ARG, "moe_gate_up: bad w_up / expert_offsets / num_experts");
     if (intermediate_size % 128 != 0)
         return set_error(JJO_ERR_INVALID_ARG, "moe_gate_up: intermediate_size must be a multiple of 128");
+    if ((rc = check_grouped_grid(n_routes, num_experts)) != JJO_OK) return rc;
     if ((rc = require_gfx950()) != JJO_OK) return rc;
     hipError_t e = launch_gemm_mfma_grouped(w_gate, x_q8_1_permuted, expert_offsets, num_experts, nullptr, gate_up,
                                             hidden_size, 2 * intermediate_size, n_routes, (hipStream_t)stream, w_up,
@@ -638,8 +651,8 @@ int moe_q4_0_gate_up_device(void *stream, const void *w_gate, const void *w_up, 
 int moe_combine_device(void *stream, const float *expert_out, const int32_t *dst_of_route,
                        const float *route_weights, float *y, int num_tokens, int hidden_size, int top_k) {
     clear_error();
-    if (num_tokens <= 0 || hidden_size <= 0 || hidden_size % 4 != 0 || top_k <= 0)
-        return set_error(JJO_ERR_INVALID_ARG, "moe_combine: num_tokens, top_k > 0 and hidden_size %% 4 == 0");
+    if (num_tokens <= 0 || num_tokens > 65535 || hidden_size <= 0 || hidden_size % 4 != 0 || top_k <= 0)
+        return set_error(JJO_ERR_INVALID_ARG, "moe_combine: 0 < num_tokens <= 65535, top_k > 0 and hidden_size %% 4 == 0");
     if (expert_out == nullptr || dst_of_route == nullptr || route_weights == nullptr || y == nullptr ||
         !aligned(expert_out, 16) || !aligned(y, 16))
         return set_error(JJO_ERR_INVALID_ARG, "moe_combine: non-null buffers, 16-byte aligned expert_out and y");

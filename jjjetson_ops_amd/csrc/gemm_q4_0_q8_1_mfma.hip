@@ -96,7 +96,10 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
         m0 = -1;
         m_end = 0;
         for (; e < n_experts; ++e) {
-            const int beg = expert_offsets[e], end = expert_offsets[e + 1];
+            // Clamped to [0, M] and to beg <= end: a malformed table yields fewer
+            // tiles, never an access outside the activation and output buffers.
+            const int beg = min(max(expert_offsets[e], 0), M);
+            const int end = min(max(expert_offsets[e + 1], beg), M);
             const int tiles = (end - beg + BM - 1) / BM;
             if (t < tiles) {
                 m0 = beg + t * BM;

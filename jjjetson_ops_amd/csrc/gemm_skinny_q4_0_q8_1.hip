@@ -91,12 +91,6 @@ struct Lds {
     static_assert(kRedBytes <= kBytes, "reduction area must fit the rings");
 };
 
-#ifdef JJO_SKINNY_TRACE
-__device__ unsigned long long g_skinny_trace[4096 * 8][16];
-#define TR(i) if (lane == 0 && blockIdx.x * KW + wave < 4096 * 8) g_skinny_trace[blockIdx.x * KW + wave][i] = __builtin_amdgcn_s_memrealtime()
-#else
-#define TR(i)
-#endif
 
 template <int RT, int CT, int P, int KW>
 __global__ __launch_bounds__(64 * KW) void gemm_skinny_kernel(const uint8_t *__restrict__ w,
@@ -261,18 +255,14 @@ __global__ __launch_bounds__(64 * KW) void gemm_skinny_kernel(const uint8_t *__r
         }
     };
 
-    TR(0);
     if (n_my > 0) {
         const int pre = min(P, n_my);
         for (int s = 0; s < pre; ++s) issue(s);
-        TR(1);
         for (int s = 0; s < n_my; ++s) {
             const int ahead = min(P, n_my - s) - 1;  // stages issued after s
             vm_wait(ahead * per_stage);
             __builtin_amdgcn_sched_barrier(0);
-            if (s < 6) { TR(2 + 2 * s); }
             consume(s);
-            if (s < 6) { TR(3 + 2 * s); }
             __builtin_amdgcn_sched_barrier(0);
             if (s + P < n_my) {
                 JJO_LGKM0();  // slot s % P fully read before it is refilled
@@ -283,7 +273,6 @@ __global__ __launch_bounds__(64 * KW) void gemm_skinny_kernel(const uint8_t *__r
     }
 
     // K-slice partials -> LDS (over the rings), summed in slice order by wave 0.
-    TR(14);
     __syncthreads();
     f32x4 *red = reinterpret_cast<f32x4 *>(smem);
 #pragma unroll
@@ -309,7 +298,6 @@ __global__ __launch_bounds__(64 * KW) void gemm_skinny_kernel(const uint8_t *__r
                 }
             }
     }
-    TR(15);
 }
 
 template <int RT, int CT, int P, int KW>
@@ -322,12 +310,9 @@ hipError_t launch_rcp(const void *w, const void *xq, float *y, int K, int N, int
 
 }  // namespace
 
-#ifndef JJO_SKINNY_RT
-#define JJO_SKINNY_RT 2
-#endif
-#ifndef JJO_SKINNY_P
-#define JJO_SKINNY_P 2
-#endif
+// Row tiles per workgroup on large-N matrices and LDS ring depth per wave.
+constexpr int kSkinnyRt = 2;
+constexpr int kSkinnyP = 2;
 
 bool gemm_skinny_supported(const void *w, const void *xq, int K, int M) {
     return K % 256 == 0 && M >= 1 && M <= kSkinnyMaxBatch && ((uintptr_t)w & 15) == 0 && ((uintptr_t)xq & 15) == 0;
@@ -339,15 +324,10 @@ hipError_t launch_gemm_skinny(const void *w, const void *xq, float *y, int K, in
         // 32-row workgroups of 4 K-slice waves while that fills the chip; for short
         // matrices (N < 8192) 16-row workgroups of 8 K-slice waves (twice the
         // workgroups, each CU holding one).
-        if ((N + 31) / 32 >= 256) return launch_rcp<JJO_SKINNY_RT, 1, JJO_SKINNY_P, 4>(w, xq, y, K, N, M, stream);
-        return launch_rcp<1, 1, JJO_SKINNY_P, 8>(w, xq, y, K, N, M, stream);
+        if ((N + 31) / 32 >= 256) return launch_rcp<kSkinnyRt, 1, kSkinnyP, 4>(w, xq, y, K, N, M, stream);
+        return launch_rcp<1, 1, kSkinnyP, 8>(w, xq, y, K, N, M, stream);
     }
-    return launch_rcp<JJO_SKINNY_RT, 2, JJO_SKINNY_P, 4>(w, xq, y, K, N, M, stream);
+    return launch_rcp<kSkinnyRt, 2, kSkinnyP, 4>(w, xq, y, K, N, M, stream);
 }
 
-#ifdef JJO_SKINNY_TRACE
-extern "C" int jjo_skinny_trace(void *host, size_t bytes) {
-    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_skinny_trace), bytes, 0, hipMemcpyDeviceToHost);
-}
-#endif
 }  // namespace jjo

@@ -431,36 +431,22 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
 // Row groups per workgroup (the activation staging of a workgroup is shared by
 // its RG row groups of U rows).  Single-token decode favours wide workgroups of
 // short row groups; multi-token batches favour four row groups of four rows.
-#ifndef JJO_GEMV1_RG1
-#define JJO_GEMV1_RG1 8
-#endif
-#ifndef JJO_GEMV1_U
-#define JJO_GEMV1_U 2
-#endif
-#ifndef JJO_GEMV1_RG3
-#define JJO_GEMV1_RG3 4
-#endif
-#ifndef JJO_GEMVM_RG1
-#define JJO_GEMVM_RG1 4
-#endif
-#ifndef JJO_GEMV4_U
-#define JJO_GEMV4_U 4
-#endif
+constexpr int kRg1 = 8;    // row groups per workgroup, Q8_1-input decode (M=1, one K slice)
+constexpr int kU1 = 2;     // rows per wave, Q8_1-input decode
+constexpr int kRg1Js3 = 4; // row groups at M=1 with three K slices
+constexpr int kRgM = 4;    // row groups, batches 2..8 (one K slice)
+constexpr int kU4 = 4;     // rows per wave at batch 4
 // The fused decode step (fp32 x quantized in every workgroup) prefers fewer,
 // deeper workgroups: four rows per wave, four row groups (K <= 4096), which halves
 // the workgroups that re-read and re-quantize x (7.22 against 7.44 us at K=4096,
 // N=11008 on one box; the Q8_1-input kernel is faster with two rows per wave).
-#ifndef JJO_GEMV1F_U
-#define JJO_GEMV1F_U 4
-#endif
-#ifndef JJO_GEMV1F_RG1
-#define JJO_GEMV1F_RG1 4
-#endif
+constexpr int kU1F = 4;
+constexpr int kRg1F = 4;
 template <int M, int JS, bool FUSED = false>
 constexpr int rg_for() {
-    if (M == 1 && FUSED && JS == 1) return JJO_GEMV1F_RG1;
-    if (M == 1) return JS == 1 ? JJO_GEMV1_RG1 : JS == 2 ? 4 : JS == 3 ? JJO_GEMV1_RG3 : 2;
-    return JS == 1 ? JJO_GEMVM_RG1 : JS == 2 ? 2 : 1;
+    if (M == 1 && FUSED && JS == 1) return kRg1F;
+    if (M == 1) return JS == 1 ? kRg1 : JS == 2 ? 4 : JS == 3 ? kRg1Js3 : 2;
+    return JS == 1 ? kRgM : JS == 2 ? 2 : 1;
 }
 
 template <int M, int U, int JS, bool FUSED, int EARLY>
@@ -507,10 +493,10 @@ hipError_t launch_m(const void *w, const void *xin, uint8_t *xq_out, float *y, i
 hipError_t launch_gemv_dot4(const void *w, const void *xq, float *y, int K, int N, int M,
                             hipStream_t stream) {
     switch (M) {
-        case 1: return launch_m<1, JJO_GEMV1_U, false>(w, xq, nullptr, y, K, N, stream);
+        case 1: return launch_m<1, kU1, false>(w, xq, nullptr, y, K, N, stream);
         case 2: return launch_m<2, 2, false>(w, xq, nullptr, y, K, N, stream);
         case 3: return launch_m<3, 4, false>(w, xq, nullptr, y, K, N, stream);
-        case 4: return launch_m<4, JJO_GEMV4_U, false>(w, xq, nullptr, y, K, N, stream);
+        case 4: return launch_m<4, kU4, false>(w, xq, nullptr, y, K, N, stream);
         case 5: return launch_m<5, 2, false>(w, xq, nullptr, y, K, N, stream);
         case 6: return launch_m<6, 2, false>(w, xq, nullptr, y, K, N, stream);
         case 7: return launch_m<7, 2, false>(w, xq, nullptr, y, K, N, stream);
@@ -521,7 +507,7 @@ hipError_t launch_gemv_dot4(const void *w, const void *xq, float *y, int K, int 
 
 hipError_t launch_gemv_fused(const void *w, const float *x, void *xq_out, float *y, int K, int N,
                              hipStream_t stream) {
-    return launch_m<1, JJO_GEMV1F_U, true>(w, x, (uint8_t *)xq_out, y, K, N, stream);
+    return launch_m<1, kU1F, true>(w, x, (uint8_t *)xq_out, y, K, N, stream);
 }
 
 }  // namespace jjo

@@ -15,6 +15,8 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <sys/stat.h>
+#include <unistd.h>
 
 #include <algorithm>
 #include <cmath>
@@ -420,12 +422,17 @@ int describe(const Header &h, const Meta &m, const char *path, int *dtype, std::
     const auto it = h.metadata.find(kQ4KeyPrefix + m.name);
     const bool q4 = it != h.metadata.end() && it->second == kQ4Marker;
     if (m.dtype == "F32" && !q4) {
+        if (numel > INT64_MAX / 4)
+            return set_error(JJO_ERR_INVALID_ARG, "%s: tensor %s is too large", path, m.name.c_str());
         *dtype = JJO_WEIGHT_DTYPE_F32;
         *dims = m.shape;
         *nbytes = numel * 4;
     } else if (m.dtype == "U8" && q4) {
         if (m.shape.size() != 3 || m.shape[2] != JJO_BLOCK_Q4_0_BYTES)
             return set_error(JJO_ERR_INVALID_ARG, "%s: Q4_0 tensor %s must have shape [rows, cols/32, 18]", path,
+                             m.name.c_str());
+        if (m.shape[1] > INT64_MAX / JJO_QK4_0 || q4_0_bytes(m.shape[0], m.shape[1] * JJO_QK4_0) != numel)
+            return set_error(JJO_ERR_INVALID_ARG, "%s: Q4_0 tensor %s has an unsupported shape", path,
                              m.name.c_str());
         *dtype = JJO_WEIGHT_DTYPE_Q4_0;
         *dims = {m.shape[0], m.shape[1] * JJO_QK4_0};
@@ -644,20 +651,34 @@ int safetensors_quantize_q4_0(const char *in_path, const char *out_path, const c
         out_metas.push_back(std::move(m));
     }
     const std::string hdr = make_header(out_metas, out_md);
+    // Written to a temporary file beside out_path and renamed over it only once
+    // complete: a failure leaves no partial output, and an existing out_path stays
+    // intact until then.
+    struct stat st_in, st_out;
+    if (fstat(fileno(in.f), &st_in) == 0 && stat(out_path, &st_out) == 0 && st_in.st_dev == st_out.st_dev &&
+        st_in.st_ino == st_out.st_ino)
+        return set_error(JJO_ERR_INVALID_ARG, "%s: output path names the input file", out_path);
+    const std::string tmp_path = std::string(out_path) + ".tmp" + std::to_string((long long)getpid());
     File out;
-    out.f = fopen(out_path, "wb");
-    if (out.f == nullptr) return set_error(JJO_ERR_INVALID_ARG, "cannot create %s: %s", out_path, strerror(errno));
+    out.f = fopen(tmp_path.c_str(), "wb");
+    if (out.f == nullptr) return set_error(JJO_ERR_INVALID_ARG, "cannot create %s: %s", tmp_path.c_str(), strerror(errno));
+    auto fail = [&](int code) {
+        if (out.f != nullptr) fclose(out.f);
+        out.f = nullptr;
+        unlink(tmp_path.c_str());
+        return code;
+    };
     uint8_t len8[8];
     for (int i = 0; i < 8; ++i) len8[i] = (uint8_t)(((uint64_t)hdr.size() >> (8 * i)) & 0xff);
-    if ((rc = write_all(out.f, len8, 8, out_path)) != JJO_OK) return rc;
-    if ((rc = write_all(out.f, hdr.data(), hdr.size(), out_path)) != JJO_OK) return rc;
+    if ((rc = write_all(out.f, len8, 8, out_path)) != JJO_OK) return fail(rc);
+    if ((rc = write_all(out.f, hdr.data(), hdr.size(), out_path)) != JJO_OK) return fail(rc);
     // One tensor in memory at a time.
     std::vector<uint8_t> src, dst;
     for (size_t i = 0; i < h.tensors.size(); ++i) {
         const Meta &m = h.tensors[i];
         src.resize((size_t)nbytes[i]);
         if (!read_at(in.f, base + m.begin, src.data(), (uint64_t)nbytes[i]))
-            return set_error(JJO_ERR_INVALID_ARG, "%s: cannot read tensor %s", in_path, m.name.c_str());
+            return fail(set_error(JJO_ERR_INVALID_ARG, "%s: cannot read tensor %s", in_path, m.name.c_str()));
         if (conv[i]) {
             dst.resize((size_t)q4_0_bytes(dims[i][0], dims[i][1]));
             quantize_threads(reinterpret_cast<const float *>(src.data()), dst.data(),
@@ -666,13 +687,14 @@ int safetensors_quantize_q4_0(const char *in_path, const char *out_path, const c
         } else {
             rc = write_all(out.f, src.data(), src.size(), out_path);
         }
-        if (rc != JJO_OK) return rc;
+        if (rc != JJO_OK) return fail(rc);
     }
-    if (fclose(out.f) != 0) {
-        out.f = nullptr;
-        return set_error(JJO_ERR_INVALID_ARG, "%s: close failed", out_path);
-    }
+    const int close_rc = fclose(out.f);
     out.f = nullptr;
+    if (close_rc != 0) return fail(set_error(JJO_ERR_INVALID_ARG, "%s: close failed", out_path));
+    if (rename(tmp_path.c_str(), out_path) != 0)
+        return fail(set_error(JJO_ERR_INVALID_ARG, "cannot rename %s to %s: %s", tmp_path.c_str(), out_path,
+                              strerror(errno)));
     return JJO_OK;
 }
 

@@ -461,3 +461,30 @@ def test_q8_1_tie_inputs_pin_the_rounded_product():
     p = x[slots].astype(np.float64) * dinv[slots // 32].astype(np.float64)
     fused = np.trunc((p + np.sign(p) * C_AWAY).astype(np.float32)).astype(np.int64)
     assert np.all(np.abs(fused - qexp) == 1)
+
+
+def test_config1_plumbing_oracle_against_dequantized_product():
+    """BASELINE config 1 (M=1, K=N=4096, seed 0) on the CPU path: the oracle's y differs
+    from the dequantized product (dequant W).(dequant x) only by the reference's sum
+    term, 8*d_w*(d_x*sum(q) - s) per block, and tracks the unquantized fp32 W.x at the
+    quantization level."""
+    K = N = 4096
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    wf = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    w = c_oracle.quantize_q4_0(wf)
+    xq = c_oracle.quantize_q8_1(x, [K, 1])
+    y = c_oracle.matmul(w, xq, K, N, 1)[0].astype(np.float64)
+    qs, d, s = c_oracle.parse_q8_1(xq, K // 128)
+    qs = qs.reshape(-1).astype(np.float64)
+    dx = d.reshape(-1).astype(np.float64)
+    sx = s.reshape(-1).astype(np.float64)
+    wdeq = q4_0.dequantize_q4_0_np(w, N, K).astype(np.float64)
+    dw = w.reshape(N, K // 32, 18)[:, :, 0:2].copy().view(np.float16)[..., 0].astype(np.float64)
+    corr = 8.0 * dw @ (dx * qs.reshape(-1, 32).sum(axis=1) - sx)
+    deq = wdeq @ (qs * np.repeat(dx, 32))
+    # exact identity up to fp32 evaluation error of y
+    np.testing.assert_allclose(y, deq + corr, rtol=1e-5, atol=1e-5)
+    assert np.abs(corr).max() > 1e-6  # the sum term is really there
+    dense = wf.astype(np.float64) @ x[0].astype(np.float64)
+    assert np.linalg.norm(y - dense) / np.linalg.norm(dense) < 0.15

@@ -254,3 +254,40 @@ def test_repacker_streams_and_quantizes(tmp_path):
         W.quantize_file(src, out2, names=["nope"])
     with pytest.raises(RuntimeError, match="not a 2-D F32"):
         W.quantize_file(src, out2, names=["layer0.w_input_layernorm"])
+
+
+def test_overflowing_shapes_are_rejected(tmp_path):
+    """A header whose shape overflows the byte count (numel*4 for F32, cols*32 for
+    Q4_0) must not wrap around to a size that matches its data_offsets."""
+    p = tmp_path / "big.safetensors"
+    a, b = 5 * 5581 * 8681, 49477 * 384773   # a*b = 2^62 + 1: a*b*4 wraps to 4 in 64 bits
+    assert a * b == (1 << 62) + 1
+    _raw_file(p, {"a": {"dtype": "F32", "shape": [a, b], "data_offsets": [0, 4]}}, b"\0" * 4)
+    with pytest.raises(RuntimeError, match="too large|unsupported shape"):
+        W.read_safetensors(p)
+    c = (1 << 58) + 1                      # cols/32 blocks whose cols*32 overflows int64
+    _raw_file(p, {"__metadata__": {"q4_0:w": "Q4_0"},
+                  "w": {"dtype": "U8", "shape": [1, c, 18], "data_offsets": [0, 18]}}, b"\0" * 18)
+    with pytest.raises(RuntimeError, match="unsupported shape"):
+        W.read_safetensors(p)
+
+
+def test_repacker_refuses_in_place_and_leaves_no_partial_file(tmp_path):
+    from safetensors.numpy import save_file
+    src = tmp_path / "f32.safetensors"
+    save_file({"w": np.ones((4, 64), np.float32)}, str(src))
+    before = src.read_bytes()
+    with pytest.raises(RuntimeError, match="names the input file"):
+        W.quantize_file(src, src)
+    assert src.read_bytes() == before
+    # a failing run (unknown tensor name) writes nothing at out_path
+    out = tmp_path / "q.safetensors"
+    with pytest.raises(RuntimeError, match="no tensor named"):
+        W.quantize_file(src, out, names=["nope"])
+    assert not out.exists()
+    assert sorted(p.name for p in tmp_path.iterdir()) == ["f32.safetensors"]
+    # a successful run replaces an existing output atomically
+    out.write_bytes(b"old")
+    W.quantize_file(src, out)
+    assert W.read_safetensors(out)["w"].dtype == W.Q4_0
+    assert sorted(p.name for p in tmp_path.iterdir()) == ["f32.safetensors", "q.safetensors"]
