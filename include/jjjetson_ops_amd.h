@@ -179,6 +179,23 @@ int linear_q4_0_forward_device(void *stream, void *quant_workspace, const float 
                                int out_features, int num_tokens);
 
 /*
+ * Allocation-free variant of linear_q4_0_forward_device.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The Q8_1
+ * activation goes to a static device buffer of linear_q4_0_noalloc_max_bytes()
+ * bytes (16 MiB: e.g. 3640 tokens at in_features 4096) that the library holds on
+ * every device it runs on until the process ends; larger batches are rejected with
+ * JJO_ERR_INVALID_ARG.  The call allocates nothing and frees nothing.  All calls
+ * on one device share that buffer: calls that overlap on one GPU (other streams,
+ * other threads) race and must be serialized by the caller.  num_tokens == 1 does
+ * not touch the buffer (the fused quantize+GEMV).  Results equal
+ * linear_q4_0_forward_device's bit for bit.
+ */
+int64_t linear_q4_0_noalloc_max_bytes(void);
+int linear_q4_0_forward_device_noalloc(void *stream, const float *input, const void *weight_q4_0, float *output,
+                                       int in_features, int out_features, int num_tokens);
+
+/*
  * Host-buffer test wrapper around linear_q4_0_forward_device, in the argument order
  * of linear_forward_host (src/cuda/linear.h:12-13).  Synchronous.
  */

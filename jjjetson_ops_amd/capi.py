@@ -48,6 +48,8 @@ EXPORTED_SYMBOLS = (
     "linear_q4_0_workspace_bytes",
     "linear_q4_0_forward_device",
     "linear_q4_0_forward_host",
+    "linear_q4_0_noalloc_max_bytes",
+    "linear_q4_0_forward_device_noalloc",
     "moe_top_k_device",
     "moe_dispatch_q8_1_device",
     "moe_q4_0_gate_up_device",
@@ -129,6 +131,10 @@ def lib() -> ctypes.CDLL:
         L.linear_q4_0_workspace_bytes.argtypes = [i32, i32]
         L.linear_q4_0_forward_device.restype = i32
         L.linear_q4_0_forward_device.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32]
+        L.linear_q4_0_noalloc_max_bytes.restype = i64
+        L.linear_q4_0_noalloc_max_bytes.argtypes = []
+        L.linear_q4_0_forward_device_noalloc.restype = i32
+        L.linear_q4_0_forward_device_noalloc.argtypes = [vp, vp, vp, vp, i32, i32, i32]
         L.linear_q4_0_forward_host.restype = i32
         L.linear_q4_0_forward_host.argtypes = [vp, vp, vp, i32, i32, i32]
         L.moe_top_k_device.restype = i32
@@ -295,6 +301,18 @@ def linear_q4_0(x, w, y, in_features: int, out_features: int, num_tokens: int, w
     _check(lib().linear_q4_0_forward_device(_stream(stream), None if ws is None else _dev(ws, "ws"), _dev(x, "x"),
                                             _dev(w, "w"), _dev(y, "y"), in_features, out_features, num_tokens),
            "linear_q4_0_forward_device")
+
+
+def linear_q4_0_noalloc(x, w, y, in_features: int, out_features: int, num_tokens: int, stream=None) -> None:
+    """linear_q4_0_forward_device_noalloc: as linear_q4_0 with the library's static
+    Q8_1 buffer instead of a workspace (calls on one device must not overlap)."""
+    _check(lib().linear_q4_0_forward_device_noalloc(_stream(stream), _dev(x, "x"), _dev(w, "w"), _dev(y, "y"),
+                                                    in_features, out_features, num_tokens),
+           "linear_q4_0_forward_device_noalloc")
+
+
+def linear_q4_0_noalloc_max_bytes() -> int:
+    return int(lib().linear_q4_0_noalloc_max_bytes())
 
 
 def linear_q4_0_workspace_bytes(in_features: int, num_tokens: int) -> int:

@@ -485,6 +485,71 @@ int linear_q4_0_forward_device(void *stream, void *quant_workspace, const float 
                                         num_tokens, stream);
 }
 
+}  // extern "C"
+
+// ---------------------------------------------------------------- allocation-free engine linear
+// Scratch of linear_q4_0_forward_device_noalloc: the Q8_1 activation of a batch
+// (num_tokens * in_features/128 * 144 bytes) lives here instead of in a caller's
+// workspace.  Each device holds its own copy for the life of the process.  In host
+// code `scratch` is only a symbol handle: the device address comes from
+// hipGetSymbolAddress, once per device, and only that address is handed to
+// kernels.
+constexpr int64_t kNoAllocScratchBytes = 16ll << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+std::vector<void *> g_scratch_ptr;  // per device; nullptr until resolved
+
+// Device address of the current device's scratch, resolved on the first call there.
+int scratch_address(void **out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return set_error(JJO_ERR_NO_DEVICE, "no HIP device: %s", hipGetErrorString(e));
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if ((int)g_scratch_ptr.size() <= dev) g_scratch_ptr.resize(dev + 1, nullptr);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (p == nullptr) return set_error(JJO_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return JJO_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int64_t linear_q4_0_noalloc_max_bytes(void) { return kNoAllocScratchBytes; }
+
+int linear_q4_0_forward_device_noalloc(void *stream, const float *input, const void *weight_q4_0, float *output,
+                                       int in_features, int out_features, int num_tokens) {
+    clear_error();
+    if (in_features <= 0 || out_features <= 0 || num_tokens <= 0)
+        return set_error(JJO_ERR_INVALID_ARG, "linear_q4_0_noalloc: invalid in_features=%d out_features=%d num_tokens=%d",
+                         in_features, out_features, num_tokens);
+    if (input == nullptr || weight_q4_0 == nullptr || output == nullptr)
+        return set_error(JJO_ERR_INVALID_ARG, "linear_q4_0_noalloc: null pointer argument");
+    const int64_t need = linear_q4_0_workspace_bytes(in_features, num_tokens);
+    if (need < 0)
+        return set_error(JJO_ERR_INVALID_ARG, "linear_q4_0_noalloc: in_features=%d must be a multiple of %d",
+                         in_features, kQSuper);
+    if (need > kNoAllocScratchBytes)
+        return set_error(JJO_ERR_INVALID_ARG,
+                         "linear_q4_0_noalloc: num_tokens=%d x in_features=%d needs %lld bytes of Q8_1 scratch, more "
+                         "than the %lld-byte static buffer; use linear_q4_0_forward_device with a workspace",
+                         num_tokens, in_features, (long long)need, (long long)kNoAllocScratchBytes);
+    int rc = require_gfx950();
+    if (rc != JJO_OK) return rc;
+    // The decode step (one token) quantizes inside its GEMV and needs no scratch.
+    void *ws = nullptr;
+    if (num_tokens > 1 && (rc = scratch_address(&ws)) != JJO_OK) return rc;
+    return mat_mul_q4_0_q8_1_f32_device(weight_q4_0, input, ws, output, in_features, out_features, num_tokens,
+                                        stream);
+}
+
 int linear_q4_0_forward_host(float *input, const void *weight_q4_0, float *output, int in_features,
                              int num_tokens, int out_features) {
     clear_error();
