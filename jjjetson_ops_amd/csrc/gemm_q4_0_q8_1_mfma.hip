@@ -14,21 +14,22 @@
 //     read as fp32 is exactly 1.5*2^23 + sumi.  The epilogue is then two fp32
 //     ops per element and block, with no int->float conversion:
 //         t   = fma(D_as_float, d_x/8, -1.5*2^23 * d_x/8)   (= round(sumi*d_x)/8)
-//         acc = fma(d_w (fp16 via v_fma_mix), t, acc)
+//         acc = fma(d_w (fp32, converted once when staged), t, acc)
 //   * The "-8 * s_x" term, sum_b d_w[n,b] * s_x[m,b], is itself a contraction
 //     over blocks: one v_mfma_f32_32x32x8_f16 per 8 blocks adds
 //     sum_b d_w * (-s_x) into the same accumulator (fp16 x fp16 products are
 //     exact in fp32).  The result is y = 8 * acc (exact power-of-two scale).
-//   * Those two fp32 ops per element-block are the bound of this kernel:
-//     2 VALU lane-ops per 64 int8 MACs+adds.  On MI355X (64 fp32 lanes/clk/CU,
-//     8192 int8 ops/clk/CU) that is 4x the MFMA time, i.e. about 25% of int8
-//     peak at best.
+//   * Those two fp32 ops per element-block bound this kernel: 2 VALU lane-ops
+//     per 64 int8 MACs+adds.  gfx950 retires plain v_fma_f32 at up to 32 lanes
+//     per clock per SIMD (128 per CU) against 8192 int8 ops/clk/CU, i.e. twice
+//     the MFMA time: about 50% of int8 peak at best.  A v_fma_mix_f32 (fp16
+//     operand) issues at about half the plain rate, hence fp32 scales.
 //   * Workgroup tile 128 (weight rows) x 128 (tokens) x 256 (K per stage);
 //     four waves in 2x2, each owning 2x2 MFMA tiles of 32x32.
 //   * Weights are staged once per workgroup: raw 18-byte blocks (dwordx4
 //     loads), nibbles expanded to int8 in K order while writing LDS, scales
-//     stored twice (fp16 row-major for the f16 MFMA, and permuted so a lane's
-//     16 epilogue rows are one 32-byte run).
+//     stored twice (fp16 row-major for the f16 MFMA, and as fp32 permuted so a
+//     lane's 16 epilogue rows are one 64-byte run).
 //   * Activations use the quantizer's superblock-major layout: for a fixed
 //     superblock the 128 tokens of a tile are one contiguous 18 KB run, copied
 //     to LDS verbatim with 16-byte loads.
@@ -50,17 +51,17 @@ constexpr int KB = 4;            // 32-blocks per stage (K = 128: one Q8_1 super
 constexpr int kThreads = 256;
 
 // LDS carve-up (bytes).  Activation and weight tiles are both double-buffered:
-// 76 KB per workgroup, so two workgroups share a CU.
+// 78 KB per workgroup, so two workgroups share a CU.
 constexpr int kXsBytes = BM * kQ8BlockBytes;             // 18432 per stage: [BM][144]
 constexpr int kWqStride = KB * 32 + 16;                  // 144: one row's 4 unpacked blocks + pad
 constexpr int kWqBytes = BN * kWqStride;                 // 18432
-constexpr int kWdEpiBytes = KB * BN * 2;                 // [KB][BN] fp16, rows permuted
+constexpr int kWdEpiBytes = KB * BN * 4;                 // [KB][BN] fp32, rows permuted
 constexpr int kWdRowBytes = BN * KB * 2;                 // [BN][KB] fp16
 constexpr int kWBufBytes = kWqBytes + kWdEpiBytes + kWdRowBytes;  // one weight stage
 constexpr int kOffW = 2 * kXsBytes;
 constexpr int kOffWdEpi = kWqBytes;                      // offsets inside a weight stage
 constexpr int kOffWdRow = kWqBytes + kWdEpiBytes;
-constexpr int kSmemBytes = kOffW + 2 * kWBufBytes;       // 77824
+constexpr int kSmemBytes = kOffW + 2 * kWBufBytes;       // 79872
 constexpr int kXUnits = kXsBytes / 16;                   // 1152 16-byte units per stage
 constexpr int kXRuns = kXUnits / 64;                     // 18 wave-sized (1 KB) runs
 
@@ -184,7 +185,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
 
     auto store_w = [&](int buf, const uint32_t(&wst)[9]) {
         uint8_t *wq = smem + kOffW + buf * kWBufBytes;
-        _Float16 *wd_epi = reinterpret_cast<_Float16 *>(wq + kOffWdEpi);
+        float *wd_epi = reinterpret_cast<float *>(wq + kOffWdEpi);
         _Float16 *wd_row = reinterpret_cast<_Float16 *>(wq + kOffWdRow);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
@@ -212,7 +213,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
             *reinterpret_cast<u32x4 *>(dst) = lo;
             *reinterpret_cast<u32x4 *>(dst + 16) = hi;
             const unsigned short dh = (unsigned short)dbits;
-            reinterpret_cast<unsigned short *>(wd_epi)[b * BN + (st_row & ~31) + epi_perm(st_row & 31)] = dh;
+            wd_epi[b * BN + (st_row & ~31) + epi_perm(st_row & 31)] = __half2float(__ushort_as_half(dh));
             reinterpret_cast<unsigned short *>(wd_row)[st_row * KB + b] = dh;
         }
     };
@@ -275,7 +276,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
             uint32_t(&w_next)[9] = *[&]() { if constexpr (PAR) return &wr0; else return &wr1; }();
 
             uint8_t *wq = smem + kOffW + (c & 1) * kWBufBytes;
-            const _Float16 *wd_epi = reinterpret_cast<const _Float16 *>(wq + kOffWdEpi);
+            const float *wd_epi = reinterpret_cast<const float *>(wq + kOffWdEpi);
             const _Float16 *wd_row = reinterpret_cast<const _Float16 *>(wq + kOffWdRow);
             const uint8_t *xs = smem + (c & 1) * kXsBytes;
 
@@ -307,31 +308,34 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
                 for (int ct = 0; ct < 2; ++ct) {
                     x_scales(hdr[ct][b], dx8[ct], nb8[ct]);
                 }
-                uint32_t wv[2][8];
+                // fp32 scales: the epilogue is two plain v_fma_f32 per element
+                // (v_fma_mix_f32 on fp16 scales issues at about half their rate).
+                float wv[2][16];
     #pragma unroll
                 for (int rt = 0; rt < 2; ++rt) {
                     const int rbase = (wn * 2 + rt) * 32 + hh * 16;
-                    const u32x4 w0 = *reinterpret_cast<const u32x4 *>(wd_epi + b * BN + rbase);
-                    const u32x4 w1 = *reinterpret_cast<const u32x4 *>(wd_epi + b * BN + rbase + 8);
-                    wv[rt][0] = w0.x; wv[rt][1] = w0.y; wv[rt][2] = w0.z; wv[rt][3] = w0.w;
-                    wv[rt][4] = w1.x; wv[rt][5] = w1.y; wv[rt][6] = w1.z; wv[rt][7] = w1.w;
+    #pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const f32x4 w4 = *reinterpret_cast<const f32x4 *>(wd_epi + b * BN + rbase + 4 * j);
+                        wv[rt][4 * j] = w4.x; wv[rt][4 * j + 1] = w4.y; wv[rt][4 * j + 2] = w4.z; wv[rt][4 * j + 3] = w4.w;
+                    }
                 }
                 // Two result tiles in flight: the MFMA of the next tile overlaps the
                 // VALU epilogue of the previous one.
                 if constexpr (LIVE == 2) {
                     i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[0], bop[0], bias, 0, 0, 0);
                     i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[0], bop[1], bias, 0, 0, 0);
-                    epilogue(acc[0][0], d0, wv[0], dx8[0], nb8[0]);
+                    epilogue_f32(acc[0][0], d0, wv[0], dx8[0], nb8[0]);
                     d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[1], bop[0], bias, 0, 0, 0);
-                    epilogue(acc[0][1], d1, wv[0], dx8[1], nb8[1]);
+                    epilogue_f32(acc[0][1], d1, wv[0], dx8[1], nb8[1]);
                     d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[1], bop[1], bias, 0, 0, 0);
-                    epilogue(acc[1][0], d0, wv[1], dx8[0], nb8[0]);
-                    epilogue(acc[1][1], d1, wv[1], dx8[1], nb8[1]);
+                    epilogue_f32(acc[1][0], d0, wv[1], dx8[0], nb8[0]);
+                    epilogue_f32(acc[1][1], d1, wv[1], dx8[1], nb8[1]);
                 } else {
                     const i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[0], bop[0], bias, 0, 0, 0);
                     const i32x16 d1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[1], bop[0], bias, 0, 0, 0);
-                    epilogue(acc[0][0], d0, wv[0], dx8[0], nb8[0]);
-                    epilogue(acc[1][0], d1, wv[1], dx8[0], nb8[0]);
+                    epilogue_f32(acc[0][0], d0, wv[0], dx8[0], nb8[0]);
+                    epilogue_f32(acc[1][0], d1, wv[1], dx8[0], nb8[0]);
                 }
             }
 

@@ -36,13 +36,13 @@ constexpr int kSXRuns = kSXsBytes / 1024;                 // 9 wave-sized (1 KB)
 template <int TR>
 struct SmallTile {
     static constexpr int kWqBytes = TR * kSWqStride;
-    static constexpr int kWdEpiBytes = SKB * TR * 2;      // [SKB][TR] fp16, rows permuted per 32
+    static constexpr int kWdEpiBytes = SKB * TR * 4;      // [SKB][TR] fp32, rows permuted per 32
     static constexpr int kWdRowBytes = TR * SKB * 2;      // [TR][SKB] fp16
     static constexpr int kWBufBytes = kWqBytes + kWdEpiBytes + kWdRowBytes;
     static constexpr int kOffW = 2 * kSXsBytes;
     static constexpr int kOffWdEpi = kWqBytes;
     static constexpr int kOffWdRow = kWqBytes + kWdEpiBytes;
-    static constexpr int kSmemBytes = kOffW + 2 * kWBufBytes;  // 38912 (TR = 64), 28672 (TR = 32)
+    static constexpr int kSmemBytes = kOffW + 2 * kWBufBytes;  // 40960 (TR = 64), 29696 (TR = 32)
     // K split between wave pairs: with 32 rows the four waves are 2 token halves x
     // 2 halves of each stage's blocks, joined at the end in a fixed order.
     static constexpr int KS = TR == 64 ? 1 : 2;
@@ -112,7 +112,8 @@ __global__ __launch_bounds__(kSThreads) void gemm_q4_0_q8_1_mfma64_kernel(const 
         *reinterpret_cast<u32x4 *>(dst) = lo;
         *reinterpret_cast<u32x4 *>(dst + 16) = hi;
         const unsigned short dh = (unsigned short)dbits;
-        reinterpret_cast<unsigned short *>(wq + kSOffWdEpi)[st_blk * SBN + (st_row & ~31) + epi_perm(st_row & 31)] = dh;
+        reinterpret_cast<float *>(wq + kSOffWdEpi)[st_blk * SBN + (st_row & ~31) + epi_perm(st_row & 31)] =
+            __half2float(__ushort_as_half(dh));
         reinterpret_cast<unsigned short *>(wq + kSOffWdRow)[st_row * SKB + st_blk] = dh;
     };
 
@@ -185,13 +186,14 @@ __global__ __launch_bounds__(kSThreads) void gemm_q4_0_q8_1_mfma64_kernel(const 
             aop = *reinterpret_cast<const i32x4 *>(wq + row * kSWqStride + b * 32 + 16 * hh);
             bop = *reinterpret_cast<const i32x4 *>(xs + col * kQ8BlockBytes + 16 + 32 * b + 16 * hh);
         };
-        auto scales = [&](int b, uint32_t(&wv)[8]) {
-            const _Float16 *wd_epi = reinterpret_cast<const _Float16 *>(wq + kSOffWdEpi);
+        auto scales = [&](int b, float(&wv)[16]) {
+            const float *wd_epi = reinterpret_cast<const float *>(wq + kSOffWdEpi);
             const int rbase = wn * 32 + hh * 16;
-            const u32x4 w0 = *reinterpret_cast<const u32x4 *>(wd_epi + b * SBN + rbase);
-            const u32x4 w1 = *reinterpret_cast<const u32x4 *>(wd_epi + b * SBN + rbase + 8);
-            wv[0] = w0.x; wv[1] = w0.y; wv[2] = w0.z; wv[3] = w0.w;
-            wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f32x4 w4 = *reinterpret_cast<const f32x4 *>(wd_epi + b * SBN + rbase + 4 * j);
+                wv[4 * j] = w4.x; wv[4 * j + 1] = w4.y; wv[4 * j + 2] = w4.z; wv[4 * j + 3] = w4.w;
+            }
         };
         const int bb = kh * kBlocksPerWave;  // this wave's first block of the stage
         i32x4 a0, b0, a1, b1;
@@ -204,11 +206,11 @@ __global__ __launch_bounds__(kSThreads) void gemm_q4_0_q8_1_mfma64_kernel(const 
                 operands(bb + j + 1, a1, b1);
                 d_next = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, b1, bias, 0, 0, 0);
             }
-            uint32_t wv[8];
+            float wv[16];
             scales(bb + j, wv);
             float dx8, nb8;
             x_scales(hdr[bb + j], dx8, nb8);
-            epilogue(acc, d_prev, wv, dx8, nb8);
+            epilogue_f32(acc, d_prev, wv, dx8, nb8);
             if (j + 1 < kBlocksPerWave) d_prev = d_next;
         }
         // sum_b d_w * (-s_x) over the stage's 4 blocks on the f16 MFMA (K = 8: the

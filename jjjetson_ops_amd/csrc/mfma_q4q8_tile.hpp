@@ -21,6 +21,7 @@ namespace {
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));           // 16-B aligned
@@ -40,6 +41,17 @@ constexpr float kBias = 12582912.0f;
 __device__ __forceinline__ int epi_perm(int r) {
     const int q = r >> 3, h = (r >> 2) & 1, i = r & 3;
     return h * 16 + q * 4 + i;
+}
+
+// Epilogue of one 32x32 int MFMA tile with fp32 scales: acc += d_w * round(sumi * d_x / 8)
+// as two plain v_fma_f32 per element (v_fma_mix_f32 issues at about half their rate).
+__device__ __forceinline__ void epilogue_f32(f32x16 &acc, const i32x16 &d, const float (&wv)[16], float dx8,
+                                             float nb8) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+        const float t = fmaf(__int_as_float(d[v]), dx8, nb8);
+        acc[v] = fmaf(wv[v], t, acc[v]);
+    }
 }
 
 // Epilogue of one 32x32 int MFMA tile: acc += d_w * round(sumi * d_x / 8).
