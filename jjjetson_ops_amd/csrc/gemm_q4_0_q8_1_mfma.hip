@@ -246,7 +246,12 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     };
     // 32-token sub-tiles of this wave that hold valid tokens (grouped tails have 0 or
     // 1): a compile-time parameter of the stage loop below, chosen once per wave.
-    const int n_live = (m0 + wm * 64 < m_end) + (m0 + wm * 64 + 32 < m_end);
+    // A tile with at most 32 valid tokens (a short tail: an expert's last few routes)
+    // runs narrow instead (LIVE = 3, grouped launches only): wave w takes weight rows
+    // 32w..32w+31 against tokens 0..31, so the four waves share the tile's one token
+    // column evenly.
+    const bool narrow = kGrouped && x_valid_tokens <= 32;  // uniform over the workgroup
+    const int n_live = narrow ? 3 : (m0 + wm * 64 < m_end) + (m0 + wm * 64 + 32 < m_end);
 
     // Pipeline, one barrier per stage.  While stage c is computed from buffers c&1,
     // X(c+1) (LDS DMA) and the weights of stages c+1 and c+2 (register sets
@@ -280,16 +285,42 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
             const _Float16 *wd_row = reinterpret_cast<const _Float16 *>(wq + kOffWdRow);
             const uint8_t *xs = smem + (c & 1) * kXsBytes;
 
-            // Activation headers (d, s) of this lane's two columns.
+            // Activation headers (d, s) of this lane's two columns (narrow: column l32).
             uint32_t hdr[2][4];
     #pragma unroll
             for (int ct = 0; ct < 2; ++ct) {
-                const int col = wm * 64 + ct * 32 + l32;
+                const int col = LIVE == 3 ? l32 : wm * 64 + ct * 32 + l32;
                 const u32x4 h = *reinterpret_cast<const u32x4 *>(xs + col * kQ8BlockBytes);
                 hdr[ct][0] = h.x; hdr[ct][1] = h.y; hdr[ct][2] = h.z; hdr[ct][3] = h.w;
             }
 
-            if constexpr (LIVE > 0) {
+            if constexpr (LIVE == 3) {
+    #pragma unroll
+            for (int b = 0; b < KB; ++b) {
+                const i32x4 bop = *reinterpret_cast<const i32x4 *>(xs + l32 * kQ8BlockBytes + 16 + 32 * b + 16 * hh);
+                const i32x4 aop =
+                    *reinterpret_cast<const i32x4 *>(wq + (wave * 32 + l32) * kWqStride + b * 32 + 16 * hh);
+                float dx8, nb8;
+                x_scales(hdr[0][b], dx8, nb8);
+                float wv[16];
+    #pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const f32x4 w4 = *reinterpret_cast<const f32x4 *>(wd_epi + b * BN + wave * 32 + hh * 16 + 4 * j);
+                    wv[4 * j] = w4.x; wv[4 * j + 1] = w4.y; wv[4 * j + 2] = w4.z; wv[4 * j + 3] = w4.w;
+                }
+                const i32x16 d0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop, bias, 0, 0, 0);
+                epilogue_f32(acc[0][0], d0, wv, dx8, nb8);
+            }
+            {
+                const f16x4 aop = *reinterpret_cast<const f16x4 *>(wd_row + (wave * 32 + l32) * KB);
+                const uint32_t *h = hdr[0];
+                uint32_t lo = ((h[0] >> 16) | (h[1] & 0xffff0000u)) ^ 0x80008000u;
+                uint32_t hi = ((h[2] >> 16) | (h[3] & 0xffff0000u)) ^ 0x80008000u;
+                if (hh) { lo = 0u; hi = 0u; }
+                const u32x2 pk = {lo, hi};
+                acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x8f16(aop, __builtin_bit_cast(f16x4, pk), acc[0][0], 0, 0, 0);
+            }
+            } else if constexpr (LIVE > 0) {
     #pragma unroll
             for (int b = 0; b < KB; ++b) {
                 i32x4 bop[2], aop[2];
@@ -385,7 +416,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
         if (c < n_stages) stage(c, std::integral_constant<int, 0>{});
         JJO_GEMM_VMCNT(0);  // the clamped loads of the last stage
     };
-    if (n_live == 2)
+    if (kGrouped && n_live == 3)
+        stage_loop(std::integral_constant<int, 3>{});
+    else if (n_live == 2)
         stage_loop(std::integral_constant<int, 2>{});
     else if (n_live == 1)
         stage_loop(std::integral_constant<int, 1>{});
@@ -393,6 +426,33 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
         stage_loop(std::integral_constant<int, 0>{});
 
     // ---- store: y[m][n] = 8 * acc ----
+    if (kGrouped && narrow) {
+        const int m = m0 + l32;
+        if (m < m_end) {
+            int out_row = m;
+            if constexpr (kGrouped) {
+                if (route_dst != nullptr) out_row = route_dst[m];
+            }
+            float *yrow = y + (size_t)out_row * N;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = n0 + wave * 32 + 8 * q + 4 * hh;
+                const float v0 = 8.0f * acc[0][0][4 * q + 0];
+                const float v1 = 8.0f * acc[0][0][4 * q + 1];
+                const float v2 = 8.0f * acc[0][0][4 * q + 2];
+                const float v3 = 8.0f * acc[0][0][4 * q + 3];
+                if (n + 3 < N && (N & 3) == 0) {
+                    *reinterpret_cast<float4 *>(yrow + n) = make_float4(v0, v1, v2, v3);
+                } else {
+                    if (n + 0 < N) yrow[n + 0] = v0;
+                    if (n + 1 < N) yrow[n + 1] = v1;
+                    if (n + 2 < N) yrow[n + 2] = v2;
+                    if (n + 3 < N) yrow[n + 3] = v3;
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
         const int m = m0 + wm * 64 + ct * 32 + l32;

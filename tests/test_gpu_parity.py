@@ -370,6 +370,35 @@ def test_grouped_moe_small(dev):
         np.testing.assert_allclose(got[sel], exp, rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("counts", [[1, 129, 0, 31, 160, 32, 33, 7], [3, 2, 1, 4]])
+def test_grouped_tail_tiles(counts, dev):
+    """Expert tails of 1..33 routes (at most 32 valid tokens runs the narrow tile
+    layout), empty experts, and a full tile followed by a tail; every output row is
+    checked against the oracle."""
+    import torch
+    E, K, N = len(counts), 512, 256
+    note(f"grouped tails counts={counts}")
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    R = int(offsets[-1])
+    x = make_x(K, R, 31)
+    xq = c_oracle.quantize_q8_1(x, [K, R])
+    ws = [make_w(N, K, 60 + e) for e in range(E)]
+    dst = np.random.default_rng(1).permutation(R).astype(np.int32)
+    y = torch.full((R * N,), float("nan"), dtype=torch.float32, device=dev)
+    capi.grouped_mat_mul(to_dev(np.concatenate(ws), dev), to_dev(xq, dev), to_dev(offsets, dev), y, K, N, R,
+                         route_dst=to_dev(dst, dev))
+    torch.cuda.synchronize()
+    got = y.cpu().numpy().reshape(R, N)
+    blocks = xq.reshape(K // 128, R, 144)
+    for e in range(E):
+        m = counts[e]
+        if m == 0:
+            continue
+        xe = np.ascontiguousarray(blocks[:, offsets[e]:offsets[e + 1]]).reshape(-1)
+        np.testing.assert_allclose(got[dst[offsets[e]:offsets[e + 1]]], c_oracle.matmul(ws[e], xe, K, N, m),
+                                   rtol=RTOL, atol=ATOL)
+
+
 # ------------------------------------------------------------------ full-size configs
 def _sample_check(w, xq, y, K, N, M, n_rows=96, n_tok=64, seed=0):
     """Oracle on a random subset of output rows and tokens (exact sub-problem)."""
