@@ -219,6 +219,30 @@ def time_moe_ffn(dev, steps, warmup):
             "mfma_frac": ops / (avg * 1e-3) / 1e12 / INT8_PEAK_TOPS,
             "weight_GBps": wbytes / (avg * 1e-3) / 1e9, "launches_per_step": 8}
 
+def time_read_floor(dev, steps, warmup, nbytes=11008 * (4096 // 32) * 18):
+    """The single-launch HBM read floor: one plain coalesced read of the decode GEMV's
+    weight bytes (K=4096, N=11008) per launch, over the same >512 MB rotation, timed
+    the same way as the GEMV (graph of back-to-back launches)."""
+    import torch
+    from jjjetson_ops_amd import capi
+    copies = max(2, math.ceil(ROTATE_BYTES / nbytes))
+    bufs = [torch.ones(nbytes, dtype=torch.uint8, device=dev) for _ in range(copies)]
+    out = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def step(i):
+        capi.read_floor(bufs[i % copies], nbytes, out)
+
+    for i in range(warmup):
+        step(i)
+    gr = _graph(step, steps)
+    gr.replay()
+    avg = _time_graph(gr) / steps
+    del gr, bufs
+    torch.cuda.empty_cache()
+    return {"name": "read_floor_25362432B", "bytes": nbytes, "us_per_launch": avg * 1e3,
+            "GBps": nbytes / (avg * 1e-3) / 1e9, "hbm_frac": nbytes / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
 def time_quantize_q4_0(dev, steps, warmup, host_threads=16):
     """The repacker's kernel: fp32 [14336, 4096] -> Q4_0 (one expert's up-projection),
     inputs rotated over > 512 MB; beside it the host quantizer on the same matrix."""
@@ -399,6 +423,8 @@ def main():
             res = time_moe(dev, max(10, args.steps // 10), 3)
         elif args.only == "moe_ffn":
             res = time_moe_ffn(dev, max(5, args.steps // 20), 2)
+        elif args.only == "read_floor":
+            res = time_read_floor(dev, args.steps, args.warmup)
         elif args.only == "quantize_q4_0":
             res = time_quantize_q4_0(dev, max(10, args.steps // 4), 3, host_threads=0)
         else:
@@ -433,6 +459,8 @@ def main():
         configs.append(time_moe(dev, max(10, args.steps // 10), 3))
         log("bench: moe ffn")
         configs.append(time_moe_ffn(dev, max(5, args.steps // 20), 2))
+        log("bench: single-launch read floor")
+        configs.append(time_read_floor(dev, args.steps, args.warmup))
         log("bench: q4_0 repacker kernel")
         configs.append(time_quantize_q4_0(dev, max(10, args.steps // 4), 3, host_threads=0 if args.no_cpu else 16))
 
@@ -451,6 +479,12 @@ def main():
             "q8_1_input_kernel": {"kernel": "gemv_q4_0_q8_1_kernel<1,2,1,8,q8_1,1>",
                                   "us_avg": head["kernel_us_avg"], "GBps": head["kernel_GBps"],
                                   "frac": head["kernel_hbm_frac"]}}
+    floor = next((c for c in configs if c["name"].startswith("read_floor")), None)
+    if floor is not None:
+        # A plain read of the same weight bytes in one launch (same rotation and
+        # timing): the practical ceiling of any single-launch GEMV at this size.
+        roof["read_floor"] = {"us": floor["us_per_launch"], "GBps": floor["GBps"], "frac": floor["hbm_frac"],
+                              "step_over_floor": head["us_per_step"] / floor["us_per_launch"]}
     gemm = next((c for c in configs if c["name"] == "prefill_m2048_k4096_n14336"), None)
     line = {
         "metric": METRIC,

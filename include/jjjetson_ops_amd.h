@@ -141,6 +141,14 @@ int mat_mul_q4_0_q8_1_block_sums_device(const void *d_w_q4_0, const void *d_x_q8
                                         void *stream);
 
 /*
+ * Diagnostic, no counterpart in the reference: one plain coalesced read of `bytes`
+ * (a multiple of 16) from d_src, the HBM read floor of a single launch that the
+ * decode GEMV's bandwidth is reported against.  d_out (4 bytes) is written only
+ * when the data's checksum hits a sentinel.
+ */
+int jjo_read_floor_device(const void *d_src, int64_t bytes, uint32_t *d_out, void *stream);
+
+/*
  * Grouped (MoE expert) matmul in one launch.  Replaces the per-expert fp32
  * moe_grouped_gemm_nt calls (src/cuda/moe/moe_pipeline_sota.cu:47-76,181-189)
  * for the Q4_0 up-projection.  Routes are sorted by expert;

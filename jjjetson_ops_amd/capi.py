@@ -45,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "mat_mul_q4_0_q8_1_device_algo",
     "mat_mul_q4_0_q8_1_block_sums_device",
     "mat_mul_q4_0_q8_1_grouped_device",
+    "jjo_read_floor_device",
     "linear_q4_0_workspace_bytes",
     "linear_q4_0_forward_device",
     "linear_q4_0_forward_host",
@@ -127,6 +128,8 @@ def lib() -> ctypes.CDLL:
         L.mat_mul_q4_0_q8_1_block_sums_device.argtypes = [vp, vp, vp, i32, i32, i32, vp]
         L.mat_mul_q4_0_q8_1_grouped_device.restype = i32
         L.mat_mul_q4_0_q8_1_grouped_device.argtypes = [vp, vp, vp, i32, vp, vp, i32, i32, i32, vp]
+        L.jjo_read_floor_device.restype = i32
+        L.jjo_read_floor_device.argtypes = [vp, i64, vp, vp]
         L.linear_q4_0_workspace_bytes.restype = i64
         L.linear_q4_0_workspace_bytes.argtypes = [i32, i32]
         L.linear_q4_0_forward_device.restype = i32
@@ -280,6 +283,12 @@ def grouped_mat_mul(w, xq, expert_offsets, y, K: int, N: int, n_routes: int, rou
     _check(lib().mat_mul_q4_0_q8_1_grouped_device(_dev(w, "w"), _dev(xq, "xq"), _dev(expert_offsets, "offsets"),
                                                   n_experts, rd, _dev(y, "y"), K, N, n_routes,
                                                   _stream(stream)), "grouped_mat_mul")
+
+
+def read_floor(src, nbytes: int, out, stream=None) -> None:
+    """jjo_read_floor_device: one plain read of nbytes of a device tensor."""
+    _check(lib().jjo_read_floor_device(_dev(src, "src"), int(nbytes), _dev(out, "out"), _stream(stream)),
+           "jjo_read_floor_device")
 
 
 def parse_q8_1(raw, n_blocks: int):

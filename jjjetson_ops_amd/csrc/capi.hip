@@ -246,6 +246,25 @@ __global__ void block_sums_kernel(const uint8_t *__restrict__ w, const uint8_t *
     out[idx] = s;
 }
 
+// Diagnostic: a plain coalesced read of `n16` 16-byte units, four per thread, the
+// XOR of everything folded into one word (written only if it hits a sentinel, so the
+// loads cannot be dropped).  The single-launch HBM read floor the GEMV is measured
+// against.
+__global__ __launch_bounds__(256) void read_floor_kernel(const uint4 *__restrict__ p, int64_t n16,
+                                                         uint32_t *__restrict__ out) {
+    const int64_t base = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+    uint4 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t j = base + 256 * i;
+        v[i] = p[j < n16 ? j : n16 - 1];
+    }
+    uint32_t acc = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    if (acc == 0x9e3779b9u) out[0] = acc;
+}
+
 }  // namespace
 
 hipError_t launch_block_sums(const void *w, const void *xq, int32_t *sumi, int K, int N, int M,
@@ -378,6 +397,20 @@ int mat_mul_q4_0_q8_1_block_sums_device(const void *d_w_q4_0, const void *d_x_q8
     hipError_t e = launch_block_sums(d_w_q4_0, d_x_q8_1, d_sumi, ncols_k, nrows_out, batch, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "block_sums launch");
     return JJO_OK;
+}
+
+int jjo_read_floor_device(const void *d_src, int64_t bytes, uint32_t *d_out, void *stream) {
+    clear_error();
+    if (d_src == nullptr || d_out == nullptr || bytes < 16 || bytes % 16 != 0 || !aligned(d_src, 16))
+        return set_error(JJO_ERR_INVALID_ARG, "read_floor: 16-byte aligned source, bytes a positive multiple of 16");
+    const int64_t n16 = bytes / 16, blocks = (n16 + 1023) / 1024;
+    if (blocks > 0x7fffffffLL) return set_error(JJO_ERR_INVALID_ARG, "read_floor: too many bytes");
+    int rc = require_gfx950();
+    if (rc != JJO_OK) return rc;
+    hipLaunchKernelGGL(read_floor_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                       (const uint4 *)d_src, n16, d_out);
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? JJO_OK : hip_fail(e, "read_floor launch");
 }
 
 int mat_mul_q4_0_q8_1_grouped_device(const void *d_w_q4_0, const void *d_x_q8_1,

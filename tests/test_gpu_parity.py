@@ -338,6 +338,21 @@ def test_mmq_host_entry_through_pybind(dev):
         np.testing.assert_allclose(y.reshape(T, N), c_oracle.matmul(w, xq, K, N, T), rtol=RTOL, atol=ATOL)
 
 
+def test_read_floor_diagnostic(dev):
+    """The read-floor diagnostic runs on any 16-byte multiple and refuses the rest."""
+    import torch
+    note("read floor diagnostic")
+    buf = torch.ones(1 << 20, dtype=torch.uint8, device=dev)
+    out = torch.zeros(1, dtype=torch.int32, device=dev)
+    capi.read_floor(buf, buf.numel(), out)
+    capi.read_floor(buf, 16, out)
+    torch.cuda.synchronize()
+    assert int(out.item()) == 0  # the checksum of all-ones data is not the sentinel
+    for n in (0, 8, 17):
+        with pytest.raises(RuntimeError, match="read_floor"):
+            capi.read_floor(buf, n, out)
+
+
 # ------------------------------------------------------------------ grouped (MoE)
 def test_grouped_moe_small(dev):
     import torch
