@@ -91,23 +91,29 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     const uint8_t *w = w_all;
     int expert = 0;
     if constexpr (kGrouped) {
-        // Tile t of the concatenated per-expert tile lists.
+        // Tile t of the concatenated per-expert tile lists: first every tile with more
+        // than 32 tokens (expert by expert), then every short tail tile (at most 32
+        // tokens, run narrow below).  The long tiles thus start in the first rounds of
+        // the grid and the short ones fill its ragged end.
         int t = blockIdx.y;
         int e = 0;
         m0 = -1;
         m_end = 0;
-        for (; e < n_experts; ++e) {
-            // Clamped to [0, M] and to beg <= end: a malformed table yields fewer
-            // tiles, never an access outside the activation and output buffers.
-            const int beg = min(max(expert_offsets[e], 0), M);
-            const int end = min(max(expert_offsets[e + 1], beg), M);
-            const int tiles = (end - beg + BM - 1) / BM;
-            if (t < tiles) {
-                m0 = beg + t * BM;
-                m_end = end;
-                break;
+        for (int pass = 0; pass < 2 && m0 < 0; ++pass) {
+            for (e = 0; e < n_experts; ++e) {
+                // Clamped to [0, M] and to beg <= end: a malformed table yields fewer
+                // tiles, never an access outside the activation and output buffers.
+                const int beg = min(max(expert_offsets[e], 0), M);
+                const int end = min(max(expert_offsets[e + 1], beg), M);
+                const int full = (end - beg) / BM, rem = (end - beg) % BM;
+                const int tiles = pass == 0 ? full + (rem > 32) : (rem > 0 && rem <= 32);
+                if (t < tiles) {
+                    m0 = beg + (pass == 0 ? t : full) * BM;
+                    m_end = end;
+                    break;
+                }
+                t -= tiles;
             }
-            t -= tiles;
         }
         if (m0 < 0) return;  // uniform over the workgroup
         expert = e;
