@@ -385,7 +385,7 @@ def test_grouped_moe_small(dev):
         np.testing.assert_allclose(got[sel], exp, rtol=RTOL, atol=ATOL)
 
 
-@pytest.mark.parametrize("counts", [[1, 129, 0, 31, 160, 32, 33, 7], [3, 2, 1, 4]])
+@pytest.mark.parametrize("counts", [[1, 129, 0, 31, 160, 32, 33, 7], [3, 2, 1, 4], [64, 65, 0, 96, 1, 200]])
 def test_grouped_tail_tiles(counts, dev):
     """Expert tails of 1..33 routes (at most 32 valid tokens runs the narrow tile
     layout), empty experts, and a full tile followed by a tail; every output row is
@@ -404,6 +404,7 @@ def test_grouped_tail_tiles(counts, dev):
                          route_dst=to_dev(dst, dev))
     torch.cuda.synchronize()
     got = y.cpu().numpy().reshape(R, N)
+    assert not np.isnan(got).any()
     blocks = xq.reshape(K // 128, R, 144)
     for e in range(E):
         m = counts[e]
