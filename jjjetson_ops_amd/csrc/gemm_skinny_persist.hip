@@ -117,18 +117,6 @@ __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uin
     for (int k0 = 0; k0 < K; k0 += kPWinK) {
         const int win = min(kPWinK, K - k0);
         const int n_st = win / (kPStageBlocks * kQK);   // stages in the window
-        // ---- activation window -> LDS (all waves), contiguous bytes ----
-        {
-            const int xbytes = (win / kQSuper) * M * kQ8BlockBytes;
-            const uint8_t *src = xq + (size_t)(k0 / kQSuper) * M * kQ8BlockBytes;
-            const int n_chunks = xbytes / 16;
-            for (int c0 = wave * 64; c0 < n_chunks; c0 += kPW * 64) {
-                const int c = c0 + lane;
-                if (c < n_chunks) dma16(src + 16 * (size_t)c, (uint32_t)(uintptr_t)(xs + 16 * c0));
-            }
-            JJO_P_VMCNT(0);
-            __syncthreads();
-        }
         const int x_stride_sb = M * kQ8BlockBytes;  // bytes per superblock in the window
 
         // ---- this wave's items: (stage s = wave + 8j, tile t) in (s, t) order ----
@@ -150,8 +138,22 @@ __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uin
                 if (i < 2 || lane < kPItemChunks - 128) dma16(src, (uint32_t)(uintptr_t)(slot + 1024 * i));
             }
         };
+
+        // ---- activation window -> LDS (all waves), contiguous bytes; then the first
+        //      ring items, so the weight stream starts while the window lands ----
+        {
+            const int xbytes = (win / kQSuper) * M * kQ8BlockBytes;
+            const uint8_t *src = xq + (size_t)(k0 / kQSuper) * M * kQ8BlockBytes;
+            const int n_chunks = xbytes / 16;
+            for (int c0 = wave * 64; c0 < n_chunks; c0 += kPW * 64) {
+                const int c = c0 + lane;
+                if (c < n_chunks) dma16(src + 16 * (size_t)c, (uint32_t)(uintptr_t)(xs + 16 * c0));
+            }
+        }
         const int pre = min(kPRing, n_items);
         for (int it = 0; it < pre; ++it) issue(it);
+        p_vm_wait(3 * pre);  // the window's DMAs (issued first) have landed
+        __syncthreads();
 
         for (int j = 0; j < my_st; ++j) {
             const int s = wave + kPW * j;
