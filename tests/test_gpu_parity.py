@@ -415,6 +415,49 @@ def test_grouped_tail_tiles(counts, dev):
                                    rtol=RTOL, atol=ATOL)
 
 
+def test_grouped_malformed_offsets_stay_in_bounds(dev):
+    """A malformed expert table (negative start, decreasing, past n_routes) drops or
+    overlaps routes but never reads or writes outside the buffers: guard rows around
+    y keep their sentinel, and each clamped range [clamp(off[e]), clamp(off[e+1]))
+    holds expert e's result."""
+    import torch
+    K, N, R = 256, 96, 90
+    offsets = np.array([-5, 50, 30, 200, 90], dtype=np.int32)
+    E = offsets.size - 1
+    note(f"grouped malformed offsets {offsets.tolist()}")
+    x = make_x(K, R, 41)
+    xq = c_oracle.quantize_q8_1(x, [K, R])
+    ws = [make_w(N, K, 70 + e) for e in range(E)]
+    guard = 64
+    buf = torch.full((R * N + 2 * guard * N,), 12345.0, dtype=torch.float32, device=dev)
+    y = buf[guard * N: guard * N + R * N]
+    capi.grouped_mat_mul(to_dev(np.concatenate(ws), dev), to_dev(xq, dev), to_dev(offsets, dev), y, K, N, R)
+    torch.cuda.synchronize()
+    b = buf.cpu().numpy()
+    assert np.all(b[:guard * N] == 12345.0) and np.all(b[guard * N + R * N:] == 12345.0)
+    got = b[guard * N: guard * N + R * N].reshape(R, N)
+    blocks = xq.reshape(K // 128, R, 144)
+    clamp = lambda v, lo: min(max(int(v), lo), R)
+    ranges = []
+    for e in range(E):
+        beg = clamp(offsets[e], 0)
+        end = clamp(offsets[e + 1], beg)
+        ranges.append((beg, end))
+    # rows covered by exactly one expert must equal that expert's result
+    owner = np.full(R, -1)
+    count = np.zeros(R, dtype=int)
+    for e, (beg, end) in enumerate(ranges):
+        owner[beg:end] = e
+        count[beg:end] += 1
+    for e, (beg, end) in enumerate(ranges):
+        rows = np.arange(beg, end)[count[beg:end] == 1]
+        if rows.size == 0:
+            continue
+        xe = np.ascontiguousarray(blocks[:, rows]).reshape(-1)
+        np.testing.assert_allclose(got[rows], c_oracle.matmul(ws[e], xe, K, N, rows.size), rtol=RTOL, atol=ATOL)
+    assert np.isfinite(got[count > 0]).all()
+
+
 # ------------------------------------------------------------------ full-size configs
 def _sample_check(w, xq, y, K, N, M, n_rows=96, n_tok=64, seed=0):
     """Oracle on a random subset of output rows and tokens (exact sub-problem)."""
