@@ -1,4 +1,4 @@
-"""Every BASELINE configuration at its full size and seed, HIP path against the oracle.
+"""Every benchmark configuration of the path at its full size and seed, HIP path against the oracle.
 
   config 1  plumbing: M=1, K=4096, N=4096, seed 0 (x and W from one generator);
             full oracle compare through both device entries, plus a bound against

@@ -464,7 +464,7 @@ def test_q8_1_tie_inputs_pin_the_rounded_product():
 
 
 def test_config1_plumbing_oracle_against_dequantized_product():
-    """BASELINE config 1 (M=1, K=N=4096, seed 0) on the CPU path: the oracle's y differs
+    """Benchmark configuration 1 (M=1, K=N=4096, seed 0) on the CPU path: the oracle's y differs
     from the dequantized product (dequant W).(dequant x) only by the reference's sum
     term, 8*d_w*(d_x*sum(q) - s) per block, and tracks the unquantized fp32 W.x at the
     quantization level."""
