@@ -163,14 +163,12 @@ int run_mm(const void *w, const void *xq, float *y, int K, int N, int M, int alg
         const bool gemv_ok = M <= kGemvMaxBatch && K <= kGemvMaxK && (int64_t)M * (K / 64) * 80 <= 150 * 1024;
         // The GEMV wins up to batch 4 on rows of one K-slice (K <= 4096); with more
         // slices its per-token cost grows and the skinny kernel wins from batch 3.
-        // At K <= 4096 the LDS-resident skinny kernel streams weights 5-15% faster
-        // than the per-wave one (one activation copy per workgroup) from batch 12, and
-        // from batch 5 while the matrix has at most three 16-row tiles per CU
-        // (N=11008: 10.7 against 11.5 us at batch 5-8; at N=14336 it is 10% slower there).
+        // At K <= 4096 the LDS-resident skinny kernel is 4-30% faster than the
+        // per-wave one from batch 5 (N=14336: 11.2-11.6 against 12.0-14.0 us; N=11008:
+        // 9.0-9.4 against 11.5-13.4 us); at larger K the per-wave kernel is faster.
         if (gemv_ok && M <= (K <= 4096 ? kGemvPreferredBatch : 2))
             algo = JJO_ALGO_GEMV;
-        else if (K <= 4096 && (M >= 12 || (M >= 5 && (int64_t)((N + 15) / 16) <= 3 * (int64_t)device_cus())) &&
-                 gemm_skinny_persist_supported(w, xq, K, M))
+        else if (K <= 4096 && M >= 5 && gemm_skinny_persist_supported(w, xq, K, M))
             algo = JJO_ALGO_SKINNY_LDS;
         else if (gemm_skinny_supported(w, xq, K, M))
             algo = JJO_ALGO_SKINNY;

@@ -11,16 +11,19 @@
 //
 // Layout of the work (one workgroup of 8 waves per CU):
 //   * A workgroup owns T consecutive 16-row weight tiles (T <= 4) and all of K.
-//   * K is walked in windows of up to 4096 values.  The window's Q8_1 activation
-//     (M tokens, the contiguous superblock-major run of the quantizer's layout) is
-//     copied to LDS once per window by all waves; nothing else reads the
-//     activation from L2.
-//   * Wave w takes the window's 256-value stages w, w+8, ...  Per stage it loads
-//     its MFMA activation operands, (d_x/8, -1.5*2^23*d_x/8) and -s_x into
-//     registers once, then runs the stage for every tile of the workgroup.
-//   * Weights stream through a per-wave LDS ring of P items (one item = one stage
+//   * K is walked in windows of up to 4096 values.  Wave w takes the window's
+//     256-value stages w and w+8.  It copies their Q8_1 activation (M tokens x 2
+//     superblocks per stage, a contiguous run of the quantizer's superblock-major
+//     layout) into its own part of the window area, so no wave waits for another's
+//     copy.  Per stage it loads its MFMA activation operands, (d_x/8,
+//     -1.5*2^23*d_x/8) and -s_x into registers once, then runs the stage for every
+//     tile of the workgroup.
+//   * Weights stream through a per-wave LDS ring of 2 items (one item = one stage
 //     of one tile: 16 rows x 144 bytes), in (stage, tile) order, with
-//     global_load_lds_dwordx4 and explicit vmcnt waits; no barrier inside a window.
+//     global_load_lds_dwordx4 and explicit vmcnt waits.  With two items in flight
+//     per wave the items land close to issue order, so each item's compute
+//     overlaps the stream; with 4 or more in flight (or every load issued at once)
+//     most items land near the end of the stream and the compute trails it.
 //   * The 8 waves' K-slice partials of each tile are added through LDS in wave
 //     order at the end (deterministic).
 //
@@ -41,12 +44,12 @@ constexpr int kPStageBlocks = 8;                         // 256 K values per sta
 constexpr int kPRowBytes = kPStageBlocks * kQ4BlockBytes;  // 144
 constexpr int kPItemBytes = 16 * kPRowBytes;             // 2304: one stage of one tile
 constexpr int kPItemChunks = kPItemBytes / 16;           // 144 chunks of 16 bytes
-constexpr int kPRing = 4;                                // items in flight per wave
+constexpr int kPRing = 2;                                // items in flight per wave (a power of 2)
 constexpr int kPWinK = 4096;                             // K values per activation window
 constexpr int kPMaxTiles = 4;
 constexpr int kPXBytes = (kPWinK / kQSuper) * 16 * kQ8BlockBytes;   // 73728 (M = 16)
 constexpr int kPRingBytes = kPW * kPRing * kPItemBytes;             // 73728
-constexpr int kPSmemBytes = kPXBytes + kPRingBytes;                 // 147456
+constexpr int kPSmemBytes = kPXBytes + kPRingBytes;                 // 110592
 constexpr uint32_t kPBiasBits = 0x4B400000u;  // 1.5 * 2^23
 constexpr float kPBias = 12582912.0f;
 
@@ -88,7 +91,7 @@ __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uin
                                                                         float *__restrict__ y, int K, int N, int M,
                                                                         int tiles_per_wg) {
     extern __shared__ __align__(16) uint8_t smem[];
-    uint8_t *xs = smem;                     // activation window [K/128][M][144]
+    uint8_t *xs = smem;                     // activation: wave w's stages at w * kPXBytes / 8
     uint8_t *ring_all = smem + kPXBytes;
 
     const int lane = threadIdx.x & 63;
@@ -139,26 +142,27 @@ __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uin
             }
         };
 
-        // ---- activation window -> LDS (all waves), contiguous bytes; then the first
-        //      ring items, so the weight stream starts while the window lands ----
+        // ---- this wave's activation stages -> its own part of the window area ----
+        uint8_t *xw = xs + wave * (kPXBytes / kPW);
         {
-            const int xbytes = (win / kQSuper) * M * kQ8BlockBytes;
-            const uint8_t *src = xq + (size_t)(k0 / kQSuper) * M * kQ8BlockBytes;
-            const int n_chunks = xbytes / 16;
-            for (int c0 = wave * 64; c0 < n_chunks; c0 += kPW * 64) {
-                const int c = c0 + lane;
-                if (c < n_chunks) dma16(src + 16 * (size_t)c, (uint32_t)(uintptr_t)(xs + 16 * c0));
+            const int x_stage_chunks = 2 * x_stride_sb / 16;
+            for (int j = 0; j < my_st; ++j) {
+                const int s = wave + kPW * j;
+                const uint8_t *src = xq + (size_t)(k0 / kQSuper + 2 * s) * x_stride_sb;
+                uint8_t *dst = xw + j * 2 * x_stride_sb;
+                for (int c0 = 0; c0 < x_stage_chunks; c0 += 64) {
+                    const int c = c0 + lane;
+                    if (c < x_stage_chunks) dma16(src + 16 * (size_t)c, (uint32_t)(uintptr_t)(dst + 16 * c0));
+                }
             }
         }
         const int pre = min(kPRing, n_items);
         for (int it = 0; it < pre; ++it) issue(it);
-        p_vm_wait(3 * pre);  // the window's DMAs (issued first) have landed
-        __syncthreads();
+        p_vm_wait(3 * pre);  // this wave's activation DMAs (issued first) have landed
 
         for (int j = 0; j < my_st; ++j) {
-            const int s = wave + kPW * j;
-            // stage operands from the activation window (registers, reused for all tiles)
-            const uint8_t *xst = xs + (size_t)(s * 2) * x_stride_sb;  // 2 superblocks per stage
+            // stage operands from the wave's copy of stage wave + 8j (registers, reused for all tiles)
+            const uint8_t *xst = xw + j * 2 * x_stride_sb;
             long aop[kPStageBlocks];
             f32x4 dx8[kPStageBlocks], nb8[kPStageBlocks];
             f16x4 sx_op;
@@ -230,6 +234,7 @@ __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uin
                         acc[t][i] = fmaf((float)dw, tt, acc[t][i]);
                     }
                 }
+                asm volatile("" : "+v"(acc[t]));  // keep the tile's epilogue here
                 // slot it % P fully read (lgkmcnt(0)) before it is refilled
                 if (it + kPRing < n_items) {
                     __builtin_amdgcn_s_waitcnt(0xC07F);
@@ -237,11 +242,11 @@ __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uin
                 }
             }
         }
-        JJO_P_VMCNT(0);
-        __syncthreads();  // the window's activation and the rings are free again
+        JJO_P_VMCNT(0);  // the wave's activation copy and ring are free again
     }
 
     // ---- K-slice partials of each tile -> LDS, summed in wave order ----
+    __syncthreads();
     f32x4 *red = reinterpret_cast<f32x4 *>(smem);
 #pragma unroll
     for (int t = 0; t < kPMaxTiles; ++t)
