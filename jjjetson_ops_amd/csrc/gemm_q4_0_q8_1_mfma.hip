@@ -24,7 +24,7 @@
 //     per clock per SIMD (128 per CU) against 8192 int8 ops/clk/CU, i.e. twice
 //     the MFMA time: about 50% of int8 peak at best.  A v_fma_mix_f32 (fp16
 //     operand) issues at about half the plain rate, hence fp32 scales.
-//   * Workgroup tile 128 (weight rows) x 128 (tokens) x 256 (K per stage);
+//   * Workgroup tile 128 (weight rows) x 128 (tokens) x 128 (K per stage);
 //     four waves in 2x2, each owning 2x2 MFMA tiles of 32x32.
 //   * Weights are staged once per workgroup: raw 18-byte blocks (dwordx4
 //     loads), nibbles expanded to int8 in K order while writing LDS, scales
