@@ -44,7 +44,8 @@ constexpr int kPStageBlocks = 8;                         // 256 K values per sta
 constexpr int kPRowBytes = kPStageBlocks * kQ4BlockBytes;  // 144
 constexpr int kPItemBytes = 16 * kPRowBytes;             // 2304: one stage of one tile
 constexpr int kPItemChunks = kPItemBytes / 16;           // 144 chunks of 16 bytes
-constexpr int kPRing = 2;                                // items in flight per wave (a power of 2)
+constexpr int kPRing = 2;                                // items in flight per wave
+static_assert(kPRing == 2, "the per-item wait below is written for two items in flight");
 constexpr int kPWinK = 4096;                             // K values per activation window
 constexpr int kPMaxTiles = 4;
 constexpr int kPXBytes = (kPWinK / kQSuper) * 16 * kQ8BlockBytes;   // 73728 (M = 16)
@@ -58,23 +59,10 @@ static_assert(kPW * kPMaxTiles * 64 * 16 <= kPSmemBytes, "reduction area must fi
 // s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] + [15:14],
 // expcnt[6:4] = 7, lgkmcnt[11:8] = 15).
 #define JJO_P_VMCNT(n) __builtin_amdgcn_s_waitcnt(((n)&15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
-__device__ __forceinline__ void p_vm_wait(int n) {  // n wave-uniform, 0..12
-    switch (n) {
-        case 0: JJO_P_VMCNT(0); break;
-        case 1: JJO_P_VMCNT(1); break;
-        case 2: JJO_P_VMCNT(2); break;
-        case 3: JJO_P_VMCNT(3); break;
-        case 4: JJO_P_VMCNT(4); break;
-        case 5: JJO_P_VMCNT(5); break;
-        case 6: JJO_P_VMCNT(6); break;
-        case 7: JJO_P_VMCNT(7); break;
-        case 8: JJO_P_VMCNT(8); break;
-        case 9: JJO_P_VMCNT(9); break;
-        case 10: JJO_P_VMCNT(10); break;
-        case 11: JJO_P_VMCNT(11); break;
-        case 12: JJO_P_VMCNT(12); break;
-        default: JJO_P_VMCNT(0); break;
-    }
+__device__ __forceinline__ void p_vm_wait_items(int pre) {  // pre wave-uniform, 0..2; 3 DMAs per item
+    if (pre == 2) JJO_P_VMCNT(6);
+    else if (pre == 1) JJO_P_VMCNT(3);
+    else JJO_P_VMCNT(0);
 }
 
 // 16 bytes per lane, global -> LDS at m0 + 16*lane.  Inline asm so that the
@@ -125,8 +113,7 @@ __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uin
         // ---- this wave's items: (stage s = wave + 8j, tile t) in (s, t) order ----
         const int my_st = (n_st - wave + kPW - 1) / kPW;
         const int n_items = my_st * T;
-        auto issue = [&](int it) {
-            const int j = it / T, t = it - j * T;
+        auto issue = [&](int it, int j, int t) {  // item it = (stage wave + 8j, tile t)
             const int s = wave + kPW * j;
             uint8_t *slot = ring + (it % kPRing) * kPItemBytes;
             const uint8_t *base = w + (size_t)((k0 / kQK) + s * kPStageBlocks) * kQ4BlockBytes;
@@ -157,8 +144,8 @@ __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uin
             }
         }
         const int pre = min(kPRing, n_items);
-        for (int it = 0; it < pre; ++it) issue(it);
-        p_vm_wait(3 * pre);  // this wave's activation DMAs (issued first) have landed
+        for (int it = 0; it < pre; ++it) issue(it, it / T, it % T);
+        p_vm_wait_items(pre);  // this wave's activation DMAs (issued first) have landed
 
         for (int j = 0; j < my_st; ++j) {
             // stage operands from the wave's copy of stage wave + 8j (registers, reused for all tiles)
@@ -204,7 +191,7 @@ __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uin
                 // one tile at a time: no hoisting of the next tile's operand reads
                 __builtin_amdgcn_sched_barrier(0);
                 const int it = j * T + t;
-                p_vm_wait(3 * (min(kPRing, n_items - it) - 1));
+                if (it + 1 < n_items) JJO_P_VMCNT(3); else JJO_P_VMCNT(0);  // item it has landed
                 const uint8_t *slot = ring + (it % kPRing) * kPItemBytes;
                 const uint8_t *wr0 = slot + l16 * kPRowBytes;
                 // s_x term: d_w of blocks 4(g&1)..4(g&1)+3 of this lane's weight row
@@ -238,7 +225,9 @@ __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uin
                 // slot it % P fully read (lgkmcnt(0)) before it is refilled
                 if (it + kPRing < n_items) {
                     __builtin_amdgcn_s_waitcnt(0xC07F);
-                    issue(it + kPRing);
+                    int jn = j, tn = t + kPRing;  // (stage, tile) of item it + 2 without a divide
+                    while (tn >= T) { tn -= T; ++jn; }
+                    issue(it + kPRing, jn, tn);
                 }
             }
         }
