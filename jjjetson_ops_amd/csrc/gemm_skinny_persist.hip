@@ -3,11 +3,17 @@
 //
 // Math is the reference's per-block epilogue (src/cuda/mm_q4_0_q8_1.cu:71-93):
 //     y[m][n] = sum_b d_w[n,b] * (sumi[n,m,b] * d_x[m,b] - 8 * s_x[m,b])
-// evaluated exactly as in the streaming skinny kernel: v_mfma_i32_16x16x32_i8 with
-// the tokens as MFMA rows and 16 weight rows as columns, the accumulator seeded
-// with the bits of 1.5*2^23 so the result read as fp32 is 1.5*2^23 + sumi, a
-// two-op epilogue (fma with d_x/8, then v_fma_mix with the fp16 d_w), and the
-// -8*s_x term as an f16 MFMA contraction over blocks; y = 8*acc.
+// evaluated exactly as in the streaming skinny kernel: the tokens as MFMA rows and
+// 16 weight rows as columns, the accumulator seeded with the bits of 1.5*2^23 so
+// the result read as fp32 is 1.5*2^23 + sumi, a two-op epilogue (fma with d_x/8,
+// then v_fma_mix with the fp16 d_w), and the -8*s_x term as an f16 MFMA
+// contraction over blocks; y = 8*acc.
+//   * M = 9..16: one v_mfma_i32_16x16x32_i8 per block (16 token rows).
+//   * M <= 8 (PAIR): one v_mfma_i32_16x16x64_i8 per pair of blocks.  Row r is token
+//     r & 7 of block parity r >> 3 and K = 64 spans both blocks, each row's other
+//     block zeroed, so every output is still one block's exact sumi while all 16
+//     rows are useful: half the epilogue instructions per block.  The two parities'
+//     partial sums meet in the final reduction.
 //
 // Layout of the work (one workgroup of 8 waves per CU):
 //   * A workgroup owns T consecutive 16-row weight tiles (T <= 4) and all of K.
@@ -74,6 +80,7 @@ __device__ __forceinline__ void dma16(const void *src, uint32_t lds_base) {
                  : "memory");
 }
 
+template <bool PAIR>
 __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uint8_t *__restrict__ w,
                                                                         const uint8_t *__restrict__ xq,
                                                                         float *__restrict__ y, int K, int N, int M,
@@ -147,6 +154,104 @@ __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uin
         for (int it = 0; it < pre; ++it) issue(it, it / T, it % T);
         p_vm_wait_items(pre);  // this wave's activation DMAs (issued first) have landed
 
+        // After item it is consumed: refill its ring slot with item it + 2.
+        auto refill = [&](int it, int j, int t) {
+            if (it + kPRing < n_items) {
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // slot it % 2 fully read (lgkmcnt(0))
+                int jn = j, tn = t + kPRing;  // (stage, tile) of item it + 2 without a divide
+                while (tn >= T) { tn -= T; ++jn; }
+                issue(it + kPRing, jn, tn);
+            }
+        };
+        if constexpr (PAIR) {
+        // M <= 8: one v_mfma_i32_16x16x64_i8 per pair of blocks.  MFMA row r is token
+        // r & 7 of block parity r >> 3; the K range 0..63 holds the pair's two blocks,
+        // and each row's other block is zero, so every output is one block's exact
+        // sumi and all 16 output rows are useful.
+        const int ta = min(l16 & 7, M - 1);  // token of this lane's A row
+        const int pa = l16 >> 3;             // block parity of this lane's A row
+        const int kc = g & 1;                // this lane's 8-byte chunk of a block's qs
+        const int po = g >> 1;               // block parity of this lane's B operand and outputs
+        for (int j = 0; j < my_st; ++j) {
+            const uint8_t *xst = xw + j * 2 * x_stride_sb;
+            i32x4 aop[kPStageBlocks / 2];
+            float dx8[kPStageBlocks / 2][4], nb8[kPStageBlocks / 2][4];
+            f16x4 sx_op;
+            {
+#pragma unroll
+                for (int p = 0; p < kPStageBlocks / 2; ++p) {
+                    const int bb = 2 * p + pa, h = bb >> 2, jj = bb & 3;
+                    const uint8_t *xa = xst + h * x_stride_sb + ta * kQ8BlockBytes + 16 + 32 * jj + 8 * kc;
+                    const uint2 lo8 = *reinterpret_cast<const uint2 *>(xa);
+                    const uint2 hi8 = *reinterpret_cast<const uint2 *>(xa + 16);
+                    const uint32_t keep = po == pa ? 0xffffffffu : 0u;
+                    aop[p] = i32x4{(int32_t)(lo8.x & keep), (int32_t)(lo8.y & keep), (int32_t)(hi8.x & keep),
+                                   (int32_t)(hi8.y & keep)};
+                }
+                // d_x of this lane's outputs: tokens 4kc..4kc+3 of blocks 2p + po
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int m = min(4 * kc + i, M - 1);
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const uint4 v = *reinterpret_cast<const uint4 *>(xst + h * x_stride_sb + m * kQ8BlockBytes);
+#pragma unroll
+                        for (int q = 0; q < 2; ++q) {  // pair p = 2h + q: block 4h + 2q + po
+                            const uint32_t vv = q == 0 ? (po ? v.y : v.x) : (po ? v.w : v.z);
+                            const float d8 = __half2float(__ushort_as_half((unsigned short)(vv & 0xffffu))) * 0.125f;
+                            dx8[2 * h + q][i] = d8;
+                            nb8[2 * h + q][i] = -kPBias * d8;
+                        }
+                    }
+                }
+                // -s_x of the stage's 8 blocks as the f16 A operand of the s_x MFMA: rows of
+                // parity 0 only (token ta), group g < 2 holds blocks 4g..4g+3.
+                const uint4 v = *reinterpret_cast<const uint4 *>(xst + (g & 1) * x_stride_sb + ta * kQ8BlockBytes);
+                const uint32_t keep = (g < 2 && pa == 0) ? 0xffffffffu : 0u;
+                const uint32_t lo = (__builtin_amdgcn_perm(v.y, v.x, 0x07060302u) ^ 0x80008000u) & keep;
+                const uint32_t hi = (__builtin_amdgcn_perm(v.w, v.z, 0x07060302u) ^ 0x80008000u) & keep;
+                sx_op = __builtin_bit_cast(f16x4, (uint64_t)hi << 32 | lo);
+            }
+#pragma unroll
+            for (int t = 0; t < kPMaxTiles; ++t) {
+                if (t >= T) break;  // workgroup-uniform
+                __builtin_amdgcn_sched_barrier(0);
+                const int it = j * T + t;
+                if (it + 1 < n_items) JJO_P_VMCNT(3); else JJO_P_VMCNT(0);  // item it has landed
+                const uint8_t *slot = ring + (it % kPRing) * kPItemBytes;
+                const uint8_t *wr0 = slot + l16 * kPRowBytes;
+                {
+                    const _Float16 *dr = reinterpret_cast<const _Float16 *>(wr0 + (g & 1) * 4 * kQ4BlockBytes);
+                    f16x4 dw_op;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) dw_op[q] = dr[q * kQ4BlockBytes / 2];
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(sx_op, dw_op, acc[t], 0, 0, 0);
+                }
+#pragma unroll
+                for (int p = 0; p < kPStageBlocks / 2; ++p) {
+                    // qs bytes 8kc..8kc+7 of block 2p + po of this lane's weight row: at byte
+                    // 18*bb + 2 + 8kc of the row, 2 mod 4 for even blocks, 0 mod 4 for odd ones.
+                    const int off = (2 * p + po) * kQ4BlockBytes + 2 + 8 * kc;
+                    const uint32_t *pp = reinterpret_cast<const uint32_t *>(wr0 + (off & ~3));
+                    const uint32_t sh = off & 3;
+                    const uint32_t d0 = pp[0], d1 = pp[1], d2 = pp[sh ? 2 : 1];
+                    const uint32_t q0 = __builtin_amdgcn_alignbyte(d1, d0, sh);
+                    const uint32_t q1 = __builtin_amdgcn_alignbyte(d2, d1, sh);
+                    const i32x4 bop = i32x4{(int32_t)(q0 & 0x0f0f0f0fu), (int32_t)(q1 & 0x0f0f0f0fu),
+                                            (int32_t)((q0 >> 4) & 0x0f0f0f0fu), (int32_t)((q1 >> 4) & 0x0f0f0f0fu)};
+                    const _Float16 dw = *reinterpret_cast<const _Float16 *>(wr0 + (2 * p + po) * kQ4BlockBytes);
+                    const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop[p], bop, bias, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float tt = fmaf(__int_as_float(d[i]), dx8[p][i], nb8[p][i]);
+                        acc[t][i] = fmaf((float)dw, tt, acc[t][i]);
+                    }
+                }
+                asm volatile("" : "+v"(acc[t]));  // keep the tile's epilogue here
+                refill(it, j, t);
+            }
+        }
+        } else {
         for (int j = 0; j < my_st; ++j) {
             // stage operands from the wave's copy of stage wave + 8j (registers, reused for all tiles)
             const uint8_t *xst = xw + j * 2 * x_stride_sb;
@@ -222,14 +327,9 @@ __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uin
                     }
                 }
                 asm volatile("" : "+v"(acc[t]));  // keep the tile's epilogue here
-                // slot it % P fully read (lgkmcnt(0)) before it is refilled
-                if (it + kPRing < n_items) {
-                    __builtin_amdgcn_s_waitcnt(0xC07F);
-                    int jn = j, tn = t + kPRing;  // (stage, tile) of item it + 2 without a divide
-                    while (tn >= T) { tn -= T; ++jn; }
-                    issue(it + kPRing, jn, tn);
-                }
+                refill(it, j, t);
             }
+        }
         }
         JJO_P_VMCNT(0);  // the wave's activation copy and ring are free again
     }
@@ -246,8 +346,15 @@ __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uin
         f32x4 sum = red[(t * kPW + 0) * 64 + lane];
 #pragma unroll
         for (int k = 1; k < kPW; ++k) sum = sum + red[(t * kPW + k) * 64 + lane];
+        if constexpr (PAIR) {
+            // lanes g and g + 2 hold the two block parities of tokens 4(g & 1)..+3
+            f32x4 odd = red[(t * kPW + 0) * 64 + (lane ^ 32)];
+#pragma unroll
+            for (int k = 1; k < kPW; ++k) odd = odd + red[(t * kPW + k) * 64 + (lane ^ 32)];
+            sum = sum + odd;
+        }
         const int n = (tile0 + t) * 16 + l16;
-        if (n < N) {
+        if (n < N && (!PAIR || g < 2)) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int m = 4 * g + i;
@@ -266,13 +373,19 @@ bool gemm_skinny_persist_supported(const void *w, const void *xq, int K, int M) 
 hipError_t launch_gemm_skinny_persist(const void *w, const void *xq, float *y, int K, int N, int M,
                                       hipStream_t stream) {
     if (!gemm_skinny_persist_supported(w, xq, K, M)) return hipErrorInvalidValue;
-    hipError_t e = ensure_dynamic_lds((const void *)gemm_skinny_persist_kernel, kPSmemBytes);
+    const void *kern = M <= 8 ? (const void *)gemm_skinny_persist_kernel<true>
+                              : (const void *)gemm_skinny_persist_kernel<false>;
+    hipError_t e = ensure_dynamic_lds(kern, kPSmemBytes);
     if (e != hipSuccess) return e;
     const int n_tiles = (N + 15) / 16;
     const int tiles_per_wg = min(kPMaxTiles, (n_tiles + 255) / 256);
     const int blocks = (n_tiles + tiles_per_wg - 1) / tiles_per_wg;
-    hipLaunchKernelGGL(gemm_skinny_persist_kernel, dim3(blocks), dim3(64 * kPW), kPSmemBytes, stream,
-                       (const uint8_t *)w, (const uint8_t *)xq, y, K, N, M, tiles_per_wg);
+    if (M <= 8)
+        hipLaunchKernelGGL(gemm_skinny_persist_kernel<true>, dim3(blocks), dim3(64 * kPW), kPSmemBytes, stream,
+                           (const uint8_t *)w, (const uint8_t *)xq, y, K, N, M, tiles_per_wg);
+    else
+        hipLaunchKernelGGL(gemm_skinny_persist_kernel<false>, dim3(blocks), dim3(64 * kPW), kPSmemBytes, stream,
+                           (const uint8_t *)w, (const uint8_t *)xq, y, K, N, M, tiles_per_wg);
     return hipGetLastError();
 }
 
