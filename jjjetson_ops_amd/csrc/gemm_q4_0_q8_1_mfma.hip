@@ -245,8 +245,13 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     const int x_valid_tokens = min(BM, m_end - m0);
     auto zero_tail_headers = [&](int buf) {
         if (x_valid_tokens < BM) {  // uniform over the workgroup
-            if (tid >= x_valid_tokens && tid < BM)
-                *reinterpret_cast<u32x4 *>(smem + buf * kXsBytes + tid * kQ8BlockBytes) = u32x4{0u, 0u, 0u, 0u};
+            if (tid >= x_valid_tokens && tid < BM) {
+                // Zeros made here (opaque to the optimizer): a zero vector kept from the
+                // kernel start was spilled and reloaded with vmcnt(0) in every stage.
+                u32x4 z = {0u, 0u, 0u, 0u};
+                asm volatile("" : "+v"(z));
+                *reinterpret_cast<u32x4 *>(smem + buf * kXsBytes + tid * kQ8BlockBytes) = z;
+            }
             __syncthreads();
         }
     };
