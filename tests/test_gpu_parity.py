@@ -172,13 +172,14 @@ def test_gemm_skinny(K, N, M, dev):
     np.testing.assert_allclose(got, c_oracle.matmul(w, xq, K, N, M), rtol=RTOL, atol=ATOL)
 
 
-@pytest.mark.parametrize("M", [1, 3, 4, 8, 13, 16])
+@pytest.mark.parametrize("M", [1, 3, 4, 5, 7, 8, 9, 13, 16])
 @pytest.mark.parametrize("K,N", [(4096, 257), (11008, 64), (256, 5), (768, 96), (14336, 48), (4352, 257),
                                  (4096, 4100), (512, 16400)])
 def test_gemm_skinny_lds(K, N, M, dev):
     """The LDS-resident skinny kernel: K windows of 4096 (14336 = 3.5 windows, 4352 =
     a one-stage last window), 1..4 tiles per workgroup (N=4100: 2, N=16400: 4 with a
-    second round), rows and tokens past the end."""
+    second round), rows and tokens past the end; M <= 8 takes the paired-block
+    MFMA path, M = 9..16 one block per MFMA."""
     note(f"gemm skinny lds K={K} N={N} M={M}")
     w = make_w(N, K, 13 * N + K)
     x = make_x(K, M, 400 + M)
