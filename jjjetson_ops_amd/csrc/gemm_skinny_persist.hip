@@ -55,7 +55,7 @@ static_assert(kPRing == 2, "the per-item wait below is written for two items in 
 constexpr int kPWinK = 4096;                             // K values per activation window
 constexpr int kPMaxTiles = 4;
 constexpr int kPXBytes = (kPWinK / kQSuper) * 16 * kQ8BlockBytes;   // 73728 (M = 16)
-constexpr int kPRingBytes = kPW * kPRing * kPItemBytes;             // 73728
+constexpr int kPRingBytes = kPW * kPRing * kPItemBytes;             // 36864
 constexpr int kPSmemBytes = kPXBytes + kPRingBytes;                 // 110592
 constexpr uint32_t kPBiasBits = 0x4B400000u;  // 1.5 * 2^23
 constexpr float kPBias = 12582912.0f;
