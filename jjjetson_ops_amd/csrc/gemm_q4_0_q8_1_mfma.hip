@@ -233,6 +233,11 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[rt][ct][v] = 0.0f;
 
+    // Paired narrow tiles (grouped, <= 8 tokens): wave w, rows 32w + 16rg + (lane & 15).
+    f32x4 acc_p[2];
+#pragma unroll
+    for (int rg = 0; rg < 2; ++rg) acc_p[rg] = f32x4{0.f, 0.f, 0.f, 0.f};
+
     i32x16 bias;
 #pragma unroll
     for (int v = 0; v < 16; ++v) bias[v] = (int32_t)kBiasBits;
@@ -243,8 +248,11 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     // Tokens past m_end (a tail tile) hold stale LDS bytes: once an activation tile has
     // landed, their (d, s) headers are zeroed, so every product with them is zero.
     const int x_valid_tokens = min(BM, m_end - m0);
+    // At most 8 valid tokens (grouped): the paired narrow layout below masks every
+    // other token in its operands, so no headers need zeroing.
+    const bool pnarrow = kGrouped && x_valid_tokens <= 8;  // uniform over the workgroup
     auto zero_tail_headers = [&](int buf) {
-        if (x_valid_tokens < BM) {  // uniform over the workgroup
+        if (x_valid_tokens < BM && !pnarrow) {  // uniform over the workgroup
             if (tid >= x_valid_tokens && tid < BM) {
                 // Zeros made here (opaque to the optimizer): a zero vector kept from the
                 // kernel start was spilled and reloaded with vmcnt(0) in every stage.
@@ -262,7 +270,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     // 32w..32w+31 against tokens 0..31, so the four waves share the tile's one token
     // column evenly.
     const bool narrow = kGrouped && x_valid_tokens <= 32;  // uniform over the workgroup
-    const int n_live = narrow ? 3 : (m0 + wm * 64 < m_end) + (m0 + wm * 64 + 32 < m_end);
+    const int n_live = pnarrow ? 4 : narrow ? 3 : (m0 + wm * 64 < m_end) + (m0 + wm * 64 + 32 < m_end);
 
     // Pipeline, one barrier per stage.  While stage c is computed from buffers c&1,
     // X(c+1) (LDS DMA) and the weights of stages c+1 and c+2 (register sets
@@ -305,7 +313,67 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
                 hdr[ct][0] = h.x; hdr[ct][1] = h.y; hdr[ct][2] = h.z; hdr[ct][3] = h.w;
             }
 
-            if constexpr (LIVE == 3) {
+            if constexpr (LIVE == 4) {
+            // Paired narrow tile (at most 8 tokens): v_mfma_i32_16x16x64_i8 with MFMA row
+            // r = token r & 7 of block parity r >> 3 and K = the pair of blocks (2p, 2p+1),
+            // each row's other block zeroed, so every output is one block's exact sumi;
+            // all 16 output rows are useful instead of 8 of 32 columns.  Lane (l16, g4):
+            // A row l16, B column = weight row 32*wave + 16*rg + l16, K chunk
+            // 16*(g4 & 1) of block 2p + (g4 >> 1); outputs are tokens 4(g4 & 1)..+3 of
+            // block parity g4 >> 1 (the parities meet at the store).
+            const int t16 = lane & 15, g4 = lane >> 4;
+            const int ta = t16 & 7, pa = t16 >> 3;
+            const bool a_on = (g4 >> 1) == pa && ta < x_valid_tokens;
+            i32x4 p_aop[2];
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+                const i32x4 v = *reinterpret_cast<const i32x4 *>(xs + ta * kQ8BlockBytes + 16 + 32 * (2 * p + pa) +
+                                                                 16 * (g4 & 1));
+                p_aop[p] = a_on ? v : i32x4{0, 0, 0, 0};
+            }
+            float p_dx8[2][4], p_nb8[2][4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = min(4 * (g4 & 1) + i, x_valid_tokens - 1);
+                const u32x4 h = *reinterpret_cast<const u32x4 *>(xs + m * kQ8BlockBytes);
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    const uint32_t hb = (g4 >> 1) ? (p ? h.w : h.y) : (p ? h.z : h.x);
+                    x_scales(hb, p_dx8[p][i], p_nb8[p][i]);
+                }
+            }
+            // -s_x of the stage's 4 blocks on rows of parity 0 (K group 0 only; zero
+            // elsewhere, and the d_w side is finite everywhere).
+            f16x4 p_sx;
+            {
+                const u32x4 h = *reinterpret_cast<const u32x4 *>(xs + min(ta, x_valid_tokens - 1) * kQ8BlockBytes);
+                const uint32_t keep = (g4 == 0 && pa == 0 && ta < x_valid_tokens) ? 0xffffffffu : 0u;
+                const uint32_t lo = (((h.x >> 16) | (h.y & 0xffff0000u)) ^ 0x80008000u) & keep;
+                const uint32_t hi = (((h.z >> 16) | (h.w & 0xffff0000u)) ^ 0x80008000u) & keep;
+                const u32x2 pk = {lo, hi};
+                p_sx = __builtin_bit_cast(f16x4, pk);
+            }
+            const i32x4 bias4 = {bias[0], bias[1], bias[2], bias[3]};
+#pragma unroll
+            for (int rg = 0; rg < 2; ++rg) {
+                const int r = wave * 32 + rg * 16 + t16;  // weight row (MFMA column) of this lane
+                f16x4 p_dw = *reinterpret_cast<const f16x4 *>(wd_row + r * KB);
+                if (g4 != 0) p_dw = f16x4{0, 0, 0, 0};
+                acc_p[rg] = __builtin_amdgcn_mfma_f32_16x16x16f16(p_sx, p_dw, acc_p[rg], 0, 0, 0);
+#pragma unroll
+                for (int p = 0; p < 2; ++p) {
+                    const int bb = 2 * p + (g4 >> 1);
+                    const i32x4 bop = *reinterpret_cast<const i32x4 *>(wq + r * kWqStride + bb * 32 + 16 * (g4 & 1));
+                    const float dw = wd_epi[bb * BN + (r & ~31) + epi_perm(r & 31)];
+                    const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x64_i8(p_aop[p], bop, bias4, 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const float tt = fmaf(__int_as_float(d[i]), p_dx8[p][i], p_nb8[p][i]);
+                        acc_p[rg][i] = fmaf(dw, tt, acc_p[rg][i]);
+                    }
+                }
+            }
+            } else if constexpr (LIVE == 3) {
     #pragma unroll
             for (int b = 0; b < KB; ++b) {
                 const i32x4 bop = *reinterpret_cast<const i32x4 *>(xs + l32 * kQ8BlockBytes + 16 + 32 * b + 16 * hh);
@@ -427,7 +495,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
         if (c < n_stages) stage(c, std::integral_constant<int, 0>{});
         JJO_GEMM_VMCNT(0);  // the clamped loads of the last stage
     };
-    if (kGrouped && n_live == 3)
+    if (kGrouped && n_live == 4)
+        stage_loop(std::integral_constant<int, 4>{});
+    else if (kGrouped && n_live == 3)
         stage_loop(std::integral_constant<int, 3>{});
     else if (n_live == 2)
         stage_loop(std::integral_constant<int, 2>{});
@@ -437,6 +507,30 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
         stage_loop(std::integral_constant<int, 0>{});
 
     // ---- store: y[m][n] = 8 * acc ----
+    if (kGrouped && pnarrow) {  // block parities meet across lanes l and l ^ 32
+        const int t16 = lane & 15, g4 = lane >> 4;
+#pragma unroll
+        for (int rg = 0; rg < 2; ++rg) {
+            f32x4 sum;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sum[i] = acc_p[rg][i] + __shfl_xor(acc_p[rg][i], 32);
+            const int n = n0 + wave * 32 + rg * 16 + t16;
+            if (g4 < 2 && n < N) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int m = m0 + 4 * g4 + i;
+                    if (m < m_end) {
+                        int out_row = m;
+                        if constexpr (kGrouped) {
+                            if (route_dst != nullptr) out_row = route_dst[m];
+                        }
+                        y[(size_t)out_row * N + n] = 8.0f * sum[i];
+                    }
+                }
+            }
+        }
+        return;
+    }
     if (kGrouped && narrow) {
         const int m = m0 + l32;
         if (m < m_end) {

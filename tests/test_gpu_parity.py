@@ -386,11 +386,12 @@ def test_grouped_moe_small(dev):
         np.testing.assert_allclose(got[sel], exp, rtol=RTOL, atol=ATOL)
 
 
-@pytest.mark.parametrize("counts", [[1, 129, 0, 31, 160, 32, 33, 7], [3, 2, 1, 4], [64, 65, 0, 96, 1, 200]])
+@pytest.mark.parametrize("counts", [[1, 129, 0, 31, 160, 32, 33, 7], [3, 2, 1, 4], [64, 65, 0, 96, 1, 200],
+                                    [8, 9, 136, 137, 5, 6]])
 def test_grouped_tail_tiles(counts, dev):
-    """Expert tails of 1..33 routes (at most 32 valid tokens runs the narrow tile
-    layout), empty experts, and a full tile followed by a tail; every output row is
-    checked against the oracle."""
+    """Expert tails of 1..33 routes (at most 8 valid tokens run the paired-block
+    narrow layout, 9..32 the 32-wide narrow layout), empty experts, and a full tile
+    followed by a tail; every output row is checked against the oracle."""
     import torch
     E, K, N = len(counts), 512, 256
     note(f"grouped tails counts={counts}")
