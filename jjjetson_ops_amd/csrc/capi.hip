@@ -244,22 +244,18 @@ __global__ void block_sums_kernel(const uint8_t *__restrict__ w, const uint8_t *
     out[idx] = s;
 }
 
-// Diagnostic: a plain coalesced read of `n16` 16-byte units, four per thread, the
-// XOR of everything folded into one word (written only if it hits a sentinel, so the
-// loads cannot be dropped).  The single-launch HBM read floor the GEMV is measured
-// against.
+// Diagnostic: a plain coalesced read of `n16` 16-byte units, one per thread, as
+// nontemporal loads, folded into one word (written only if it hits a sentinel, so
+// the loads cannot be dropped).  The single-launch HBM read floor the GEMV is
+// measured against.  Of the read forms timed on this GPU for the GEMV's 25.4 MB
+// (1, 2, 4, 8 or 16 loads per thread, plain or nontemporal, persistent grids of
+// 256..4096 workgroups), this one is the fastest.
 __global__ __launch_bounds__(256) void read_floor_kernel(const uint4 *__restrict__ p, int64_t n16,
                                                          uint32_t *__restrict__ out) {
-    const int64_t base = (int64_t)blockIdx.x * 1024 + threadIdx.x;
-    uint4 v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int64_t j = base + 256 * i;
-        v[i] = p[j < n16 ? j : n16 - 1];
-    }
-    uint32_t acc = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    typedef uint32_t u32x4n __attribute__((ext_vector_type(4)));
+    const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const u32x4n v = __builtin_nontemporal_load(reinterpret_cast<const u32x4n *>(p + (j < n16 ? j : n16 - 1)));
+    const uint32_t acc = v.x ^ v.y ^ v.z ^ v.w;
     if (acc == 0x9e3779b9u) out[0] = acc;
 }
 
@@ -401,7 +397,7 @@ int jjo_read_floor_device(const void *d_src, int64_t bytes, uint32_t *d_out, voi
     clear_error();
     if (d_src == nullptr || d_out == nullptr || bytes < 16 || bytes % 16 != 0 || !aligned(d_src, 16))
         return set_error(JJO_ERR_INVALID_ARG, "read_floor: 16-byte aligned source, bytes a positive multiple of 16");
-    const int64_t n16 = bytes / 16, blocks = (n16 + 1023) / 1024;
+    const int64_t n16 = bytes / 16, blocks = (n16 + 255) / 256;
     if (blocks > 0x7fffffffLL) return set_error(JJO_ERR_INVALID_ARG, "read_floor: too many bytes");
     int rc = require_gfx950();
     if (rc != JJO_OK) return rc;
