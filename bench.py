@@ -5,10 +5,11 @@ K=4096 -> N=11008.  One step = quantize the fp32 activation to Q8_1 on the
 device + the Q4_0 x Q8_1 GEMV, exactly what a decode layer does per linear.
 ``value`` is effective weight GB/s of the whole step (weight bytes / step
 time).  Weight buffers rotate over > 512 MB so the 256 MB MALL cannot serve
-them.  Timed steps are captured in one HIP graph and replayed, bracketed by
-HIP events on the launch stream.  ``roofline`` is the GEMV kernel alone (a
-graph of back-to-back GEMV launches).  The other configurations are measured
-the same way and reported under ``configs``.
+them.  Exactly `steps` steps are timed back to back between HIP events on the
+launch stream, enqueued behind a device spin so that host launch cost stays
+outside the interval.  ``roofline`` is the step's one kernel (the fused GEMV).
+The other configurations are measured the same way and reported under
+``configs``.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--quick] [--no-cpu]
        python bench.py --only NAME [--calib-copy-mib N]   (profiling runs: one
@@ -59,35 +60,63 @@ def make_x(M, K, seed, dev, outliers):
     return x.contiguous()
 
 
-def _graph(fn, n):
-    """Capture n calls fn(i) into one HIP graph on torch's capture stream."""
+_SPIN_CYCLES_PER_MS = None
+
+
+def _spin_cycles_per_ms():
+    """Clock cycles of torch.cuda._sleep (a device spin kernel) per millisecond,
+    measured once with events."""
+    global _SPIN_CYCLES_PER_MS
+    if _SPIN_CYCLES_PER_MS is None:
+        import torch
+        torch.cuda._sleep(100_000)  # warm the spin kernel
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        n = 2_000_000
+        e0.record()
+        torch.cuda._sleep(n)
+        e1.record()
+        torch.cuda.synchronize()
+        _SPIN_CYCLES_PER_MS = n / max(e0.elapsed_time(e1), 1e-3)
+    return _SPIN_CYCLES_PER_MS
+
+
+def _time_steps(fn, steps, launches_per_step=1):
+    """Milliseconds for exactly `steps` calls fn(0..steps-1) on the current stream,
+    between two HIP events on that stream.
+
+    The host's launch cost is kept out of the interval: a device spin is enqueued
+    first and every step is enqueued while it runs, so e0 fires when the spin ends
+    and the interval holds the steps' kernels back to back and nothing else.  If the
+    spin ended before the last step was enqueued (e0 already complete), the GPU may
+    have waited on the host, so the measurement is repeated with a spin twice as
+    long.  (A HIP graph replay was not used: it adds a fixed ~8 us per replay on
+    the GPU, which makes the per-step figure depend on the number of steps.)"""
     import torch
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for i in range(n):
+    cyc = _spin_cycles_per_ms()
+    spin_ms = 1.0 + 0.03 * steps * launches_per_step
+    for _ in range(6):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        torch.cuda._sleep(int(cyc * spin_ms))
+        e0.record()
+        for i in range(steps):
             fn(i)
-    return g
+        starved = e0.query()
+        e1.record()
+        torch.cuda.synchronize()
+        if not starved:
+            return e0.elapsed_time(e1)
+        spin_ms *= 2
+    raise RuntimeError("bench: the host could not enqueue the steps within the device spin")
 
 
-def _time_graph(g, reps=1):
-    import torch
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(reps):
-        g.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1)  # ms
-
-
-def time_linear(name, M, K, N, seed, dev, steps, warmup, outliers=True):
+def time_linear(name, M, K, N, seed, dev, steps, warmup, outliers=True, split=False):
     """Per step: device quantize of x [M,K] + mat_mul against rotating weights.
 
-    Steps are captured in one HIP graph (launch overhead of the Python caller is not
-    part of the GPU's work) and replayed once: exactly `steps` timed steps.  A second
-    graph holds only the matmul launches, for the kernel's own average duration.
+    Exactly `steps` timed steps (see _time_steps).  A second run times only the
+    matmul launches (Q8_1 input), for the kernel's own average duration.
     """
     import torch
     from jjjetson_ops_amd import capi
@@ -95,30 +124,36 @@ def time_linear(name, M, K, N, seed, dev, steps, warmup, outliers=True):
     wbytes = N * (K // 32) * 18
     copies = max(2, math.ceil(ROTATE_BYTES / wbytes))
     ws = make_weights(N, K, seed, dev, copies)
+    if split:
+        # The load-time repack into the split layout (nibble plane + scale plane).
+        for i in range(copies):
+            t = torch.empty_like(ws[i])
+            capi.q4_0_to_split(ws[i], t, N, K)
+            ws[i] = t
+        torch.cuda.synchronize()
     x = make_x(M, K, seed + 1000, dev, outliers)
     xq = torch.empty(capi.q8_1_output_bytes([K, M]), dtype=torch.uint8, device=dev)
     y = torch.empty(M * N, dtype=torch.float32, device=dev)
 
+    mm_f32 = capi.mat_mul_split_f32 if split else capi.mat_mul_f32
+    mm_q8 = capi.mat_mul_split if split else capi.mat_mul
+
     def step(i):
         # The reference's mat_mul_q4_0_q8_1 on device pointers: quantize x into the
         # Q8_1 workspace and multiply (one fused kernel at M = 1, two kernels above).
-        capi.mat_mul_f32(ws[i % copies], x, xq, y, K, N, M)
+        mm_f32(ws[i % copies], x, xq, y, K, N, M)
 
     def mm_only(i):
-        capi.mat_mul(ws[i % copies], xq, y, K, N, M)
+        mm_q8(ws[i % copies], xq, y, K, N, M)
 
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
     capi.quantize_q8_1(x, xq, [K, M])
     torch.cuda.synchronize()
-    g_step = _graph(step, steps)
-    g_mm = _graph(mm_only, steps)
-    g_step.replay()
-    g_mm.replay()
-    ms_step = _time_graph(g_step) / steps
-    kern_ms = _time_graph(g_mm) / steps
-    del g_step, g_mm, ws
+    ms_step = _time_steps(step, steps, 1 if M == 1 else 2) / steps
+    kern_ms = _time_steps(mm_only, steps) / steps
+    del ws
     torch.cuda.empty_cache()
     alg_bytes = wbytes + M * (K // 128) * 144 + 4 * M * N
     # The fused M = 1 step reads x in fp32 and writes the Q8_1 workspace as well.
@@ -127,7 +162,8 @@ def time_linear(name, M, K, N, seed, dev, steps, warmup, outliers=True):
     return {
         "step_alg_bytes": step_bytes,
         "step_GBps": step_bytes / (ms_step * 1e-3) / 1e9,
-        "name": name, "M": M, "K": K, "N": N, "weight_bytes": wbytes, "weight_copies": copies,
+        "name": name, "M": M, "K": K, "N": N, "weight_layout": "split" if split else "block_q4_0",
+        "weight_bytes": wbytes, "weight_copies": copies,
         "ms_per_step": ms_step, "us_per_step": ms_step * 1e3, "kernel_us_avg": kern_ms * 1e3,
         "step_weight_GBps": wbytes / (ms_step * 1e-3) / 1e9,
         "kernel_GBps": alg_bytes / (kern_ms * 1e-3) / 1e9,
@@ -170,12 +206,10 @@ def time_moe(dev, steps, warmup):
 
     for i in range(warmup):
         mm(i)
-    gr = _graph(mm, steps)
-    gr.replay()
-    avg = _time_graph(gr) / steps
+    avg = _time_steps(mm, steps) / steps
     ops = 2.0 * R * N * K
     alg_bytes = wbytes + R * (K // 128) * 144 + 4 * R * N
-    del gr, ws, w_one
+    del ws, w_one
     torch.cuda.empty_cache()
     return {"name": "moe_grouped_e8_top2_t512", "routes": R, "K": K, "N": N,
             "expert_counts": counts.tolist(), "kernel_us_avg": avg * 1e3,
@@ -187,7 +221,7 @@ def time_moe(dev, steps, warmup):
 def time_moe_ffn(dev, steps, warmup):
     """The whole Q4_0 MoE FFN of the same layer shape (8 experts, top-2, 512 tokens,
     H=4096, I=14336): quantize, top-k, dispatch, gate|up, SwiGLU+quantize, down,
-    combine -- eight launches per step, captured in one graph."""
+    combine -- eight launches per step."""
     import torch
     from jjjetson_ops_amd import capi
 
@@ -206,13 +240,10 @@ def time_moe_ffn(dev, steps, warmup):
 
     for i in range(warmup):
         step(i)
-    gr = _graph(step, steps)
-    gr.replay()
-    avg = _time_graph(gr) / steps
+    avg = _time_steps(step, steps, 8) / steps
     R = T * topk
     ops = 2.0 * R * 3 * I * H
     wbytes = 3 * E * I * (H // 32) * 18  # 792 MB: every step streams past the MALL
-    del gr
     torch.cuda.empty_cache()
     return {"name": "moe_ffn_q4_0_e8_top2_t512_h4096_i14336", "routes": R, "H": H, "I": I,
             "us_per_step": avg * 1e3, "TOPS": ops / (avg * 1e-3) / 1e12,
@@ -222,7 +253,7 @@ def time_moe_ffn(dev, steps, warmup):
 def time_read_floor(dev, steps, warmup, nbytes=11008 * (4096 // 32) * 18):
     """The single-launch HBM read floor: one plain coalesced read of the decode GEMV's
     weight bytes (K=4096, N=11008) per launch, over the same >512 MB rotation, timed
-    the same way as the GEMV (graph of back-to-back launches)."""
+    the same way as the GEMV (back-to-back launches)."""
     import torch
     from jjjetson_ops_amd import capi
     copies = max(2, math.ceil(ROTATE_BYTES / nbytes))
@@ -234,10 +265,8 @@ def time_read_floor(dev, steps, warmup, nbytes=11008 * (4096 // 32) * 18):
 
     for i in range(warmup):
         step(i)
-    gr = _graph(step, steps)
-    gr.replay()
-    avg = _time_graph(gr) / steps
-    del gr, bufs
+    avg = _time_steps(step, steps) / steps
+    del bufs
     torch.cuda.empty_cache()
     return {"name": "read_floor_25362432B", "bytes": nbytes, "us_per_launch": avg * 1e3,
             "GBps": nbytes / (avg * 1e-3) / 1e9, "hbm_frac": nbytes / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS}
@@ -264,15 +293,13 @@ def time_quantize_q4_0(dev, steps, warmup, host_threads=16):
 
     for i in range(warmup):
         step(i)
-    gr = _graph(step, steps)
-    gr.replay()
-    avg = _time_graph(gr) / steps
+    avg = _time_steps(step, steps) / steps
     alg = in_bytes + out_bytes
     res = {"name": "quantize_q4_0_n14336_k4096", "rows": N, "cols": K, "us_per_launch": avg * 1e3,
            "alg_bytes_per_launch": alg, "GBps": alg / (avg * 1e-3) / 1e9,
            "hbm_frac": alg / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS}
     wh = w0.cpu().numpy()
-    del gr, ws, outs, w0
+    del ws, outs, w0
     torch.cuda.empty_cache()
     if host_threads:
         t0 = time.perf_counter()
@@ -409,6 +436,8 @@ def main():
 
     plan = [
         ("gemv_m1_k4096_n11008", 1, 4096, 11008, 1, args.steps),
+        ("gemv_m1_k4096_n11008_split", 1, 4096, 11008, 1, args.steps),
+        ("gemv_m1_k11008_n4096_split", 1, 11008, 4096, 1, args.steps),
         ("gemv_m1_k11008_n4096", 1, 11008, 4096, 1, args.steps),
         ("m4_k4096_n14336", 4, 4096, 14336, 2, args.steps),
         ("m8_k4096_n14336", 8, 4096, 14336, 2, args.steps),
@@ -432,7 +461,7 @@ def main():
             if not sel:
                 sys.exit(f"unknown config {args.only}; choose from {[p[0] for p in plan]} or moe_grouped_e8_top2_t512")
             name, M, K, N, seed, st = sel[0]
-            res = time_linear(name, M, K, N, seed, dev, st, args.warmup)
+            res = time_linear(name, M, K, N, seed, dev, st, args.warmup, split=name.endswith("_split"))
         if args.calib_copy_mib:
             # A plain device copy of known size, for scaling FETCH_SIZE / WRITE_SIZE.
             # The source is pushed out of L2 and the 256 MB MALL first by writing 1 GiB.
@@ -454,7 +483,8 @@ def main():
     if not args.quick:
         for name, M, K, N, seed, st in plan[1:]:
             log(f"bench: {name}")
-            configs.append(time_linear(name, M, K, N, seed, dev, st, max(3, args.warmup // 4)))
+            configs.append(time_linear(name, M, K, N, seed, dev, st, max(3, args.warmup // 4),
+                                       split=name.endswith("_split")))
         log("bench: moe grouped")
         configs.append(time_moe(dev, max(10, args.steps // 10), 3))
         log("bench: moe ffn")
@@ -475,7 +505,7 @@ def main():
             "frac": head["step_GBps"] / HBM_PEAK_GBS, "traffic": _traffic("gemv_m1_k4096_n11008"),
             "kernel": "gemv_q4_0_q8_1_kernel<1,4,1,4,fused,1>", "alg_bytes_per_launch": head["step_alg_bytes"],
             "kernel_us_avg": head["us_per_step"],
-            "timing": "HIP graph of back-to-back launches on the launch stream, torch.cuda.Event around the replay",
+            "timing": "back-to-back launches on the launch stream, enqueued behind a device spin, torch.cuda.Event around exactly `steps` launches",
             "q8_1_input_kernel": {"kernel": "gemv_q4_0_q8_1_kernel<1,2,1,8,q8_1,1>",
                                   "us_avg": head["kernel_us_avg"], "GBps": head["kernel_GBps"],
                                   "frac": head["kernel_hbm_frac"]}}

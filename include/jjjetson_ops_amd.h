@@ -113,6 +113,49 @@ int mat_mul_q4_0_q8_1_device(const void *d_w_q4_0, const void *d_x_q8_1, float *
 int mat_mul_q4_0_q8_1_f32_device(const void *d_w_q4_0, const float *d_x, void *d_quant_workspace,
                                  float *d_y, int ncols_k, int nrows_out, int batch, void *stream);
 
+/* ------------------------------------------------------------ split weight layout
+ * The offline repack of a Q4_0 matrix for the GPU (the "repacker to the
+ * GPU-friendly split layout" beside the Q4_0 WeightDtype of
+ * src/model/weight_loader.h:12-14).  block_q4_0 (18 B) is only 2-byte aligned
+ * (src/cuda/mm_q4_0_q8_1.cu:35-38, read with 16-bit gathers at :50-62); the split
+ * layout of an nrows x (ncols_k/32) block matrix keeps every byte but moves the
+ * scales out, so every block's nibbles are one aligned 16-byte load:
+ *     qs plane: block (n, b)'s 16 nibble bytes at (n*nb + b)*16
+ *     d plane : its fp16 scale at nrows*nb*16 + (n*nb + b)*2      (nb = ncols_k/32)
+ * Same size as the Q4_0 matrix.  Nibble order and values are block_q4_0's.
+ * The reference layout stays the interface of every entry above; the split
+ * layout is an extra, load-time format for callers that repack once.
+ */
+
+/* Bytes of a matrix in either layout (nrows*ncols_k/32*18); -1 if invalid. */
+int64_t q4_0_split_bytes(int64_t nrows, int64_t ncols_k);
+
+/* Host repackers (pure CPU, no device): block_q4_0 rows <-> split layout.
+ * Buffers must not alias. */
+int q4_0_to_split(const void *w_q4_0, void *w_split, int64_t nrows, int64_t ncols_k);
+int q4_0_from_split(const void *w_split, void *w_q4_0, int64_t nrows, int64_t ncols_k);
+
+/* Device repacker on `stream` (source 2-byte, destination 16-byte aligned, no
+ * aliasing).  Stacked expert matrices repack as one matrix of E*nrows rows. */
+int q4_0_to_split_device(const void *d_w_q4_0, void *d_w_split, int nrows, int ncols_k, void *stream);
+
+/*
+ * mat_mul_q4_0_q8_1_device (src/cuda/mm_q4_0_q8_1.cu:394, same arguments and
+ * results) on a split-layout weight (16-byte aligned).  Batch <= 8 with
+ * batch*ncols_k/32*48 <= 150 KiB and ncols_k <= 16384; other shapes return
+ * JJO_ERR_INVALID_ARG.
+ */
+int mat_mul_q4_0s_q8_1_device(const void *d_w_split, const void *d_x_q8_1, float *d_y, int ncols_k,
+                              int nrows_out, int batch, void *stream);
+
+/*
+ * mat_mul_q4_0_q8_1_f32_device on a split-layout weight: quantize d_x into
+ * d_quant_workspace and multiply.  At batch == 1 (ncols_k <= 16384) one fused
+ * kernel does both, and d_quant_workspace may be NULL.
+ */
+int mat_mul_q4_0s_q8_1_f32_device(const void *d_w_split, const float *d_x, void *d_quant_workspace,
+                                  float *d_y, int ncols_k, int nrows_out, int batch, void *stream);
+
 /* Kernel selector for mat_mul_q4_0_q8_1_device_algo. */
 #define JJO_ALGO_AUTO 0
 #define JJO_ALGO_GEMV 1 /* streaming GEMV (v_dot8 on 4-bit planes), batch <= 8 */
@@ -141,7 +184,8 @@ int mat_mul_q4_0_q8_1_block_sums_device(const void *d_w_q4_0, const void *d_x_q8
                                         void *stream);
 
 /*
- * Diagnostic, no counterpart in the reference: one plain coalesced read of `bytes`
+ * DIAGNOSTIC ONLY (a measurement probe, not part of the drop-in path; no
+ * counterpart in the reference): one plain coalesced read of `bytes`
  * (a multiple of 16) from d_src, the HBM read floor of a single launch that the
  * decode GEMV's bandwidth is reported against.  d_out (4 bytes) is written only
  * when the data's checksum hits a sentinel.
@@ -159,8 +203,9 @@ int jjo_read_floor_device(const void *d_src, int64_t bytes, uint32_t *d_out, voi
  * to d_y[route_dst[r]*nrows_out ...] (route_dst may be NULL: identity).
  * expert_offsets (device, E+1 entries) must be non-decreasing with
  * expert_offsets[0] == 0 and expert_offsets[E] == n_routes; the kernel clamps
- * every range to [0, n_routes], so a malformed table drops routes instead of
- * reading or writing outside the buffers.  (n_routes+127)/128 + n_experts must
+ * every range to [0, n_routes], so a malformed offset table drops routes instead
+ * of reading or writing outside the buffers.  route_dst is not checked: each of
+ * its entries must lie in [0, rows of d_y), or the store writes outside d_y.  (n_routes+127)/128 + n_experts must
  * not exceed 65535.
  */
 int mat_mul_q4_0_q8_1_grouped_device(const void *d_w_q4_0, const void *d_x_q8_1,
@@ -195,8 +240,9 @@ int linear_q4_0_forward_device(void *stream, void *quant_workspace, const float 
  * every device it runs on until the process ends; larger batches are rejected with
  * JJO_ERR_INVALID_ARG.  The call allocates nothing and frees nothing.  All calls
  * on one device share that buffer: calls that overlap on one GPU (other streams,
- * other threads) race and must be serialized by the caller.  num_tokens == 1 does
- * not touch the buffer (the fused quantize+GEMV).  Results equal
+ * other threads) race and must be serialized by the caller.  num_tokens == 1 with
+ * in_features <= 16384 does not touch the buffer (the fused quantize+GEMV); any
+ * other call quantizes into it.  Results equal
  * linear_q4_0_forward_device's bit for bit.
  */
 int64_t linear_q4_0_noalloc_max_bytes(void);

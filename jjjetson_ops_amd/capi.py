@@ -66,6 +66,12 @@ EXPORTED_SYMBOLS = (
     "jjo_host_tensors_find",
     "safetensors_write_file_q4_0",
     "safetensors_quantize_q4_0",
+    "q4_0_split_bytes",
+    "q4_0_to_split",
+    "q4_0_from_split",
+    "q4_0_to_split_device",
+    "mat_mul_q4_0s_q8_1_device",
+    "mat_mul_q4_0s_q8_1_f32_device",
 )
 
 WEIGHT_DTYPE_F32 = 0
@@ -172,6 +178,18 @@ def lib() -> ctypes.CDLL:
         L.safetensors_quantize_q4_0.restype = i32
         L.safetensors_quantize_q4_0.argtypes = [ctypes.c_char_p, ctypes.c_char_p,
                                                 ctypes.POINTER(ctypes.c_char_p), i32, i32]
+        L.q4_0_split_bytes.restype = i64
+        L.q4_0_split_bytes.argtypes = [i64, i64]
+        L.q4_0_to_split.restype = i32
+        L.q4_0_to_split.argtypes = [vp, vp, i64, i64]
+        L.q4_0_from_split.restype = i32
+        L.q4_0_from_split.argtypes = [vp, vp, i64, i64]
+        L.q4_0_to_split_device.restype = i32
+        L.q4_0_to_split_device.argtypes = [vp, vp, i32, i32, vp]
+        L.mat_mul_q4_0s_q8_1_device.restype = i32
+        L.mat_mul_q4_0s_q8_1_device.argtypes = [vp, vp, vp, i32, i32, i32, vp]
+        L.mat_mul_q4_0s_q8_1_f32_device.restype = i32
+        L.mat_mul_q4_0s_q8_1_f32_device.argtypes = [vp, vp, vp, vp, i32, i32, i32, vp]
         _lib = L
     return _lib
 
@@ -257,6 +275,66 @@ def mat_mul_f32(w, x, xq, y, K: int, N: int, M: int, stream=None) -> None:
     xqp = _dev(xq, "xq") if xq is not None else ctypes.c_void_p(0)
     _check(lib().mat_mul_q4_0_q8_1_f32_device(_dev(w, "w"), _dev(x, "x"), xqp, _dev(y, "y"), K, N, M,
                                               _stream(stream)), "mat_mul_q4_0_q8_1_f32_device")
+
+
+# ---------------------------------------------------------------- split weight layout
+def q4_0_to_split_host(w, nrows: int, ncols_k: int):
+    """Host repack: uint8 block_q4_0 rows -> split layout (a new uint8 ndarray)."""
+    import numpy as np
+    w = np.ascontiguousarray(w, dtype=np.uint8).reshape(-1)
+    n = int(lib().q4_0_split_bytes(nrows, ncols_k))
+    if n < 0 or w.size < n:
+        raise ValueError("invalid shape or weight buffer too small")
+    out = np.empty(n, np.uint8)
+    _check(lib().q4_0_to_split(w.ctypes.data, out.ctypes.data, nrows, ncols_k), "q4_0_to_split")
+    return out
+
+
+def q4_0_from_split_host(ws, nrows: int, ncols_k: int):
+    """Host inverse repack: split layout -> block_q4_0 rows (a new uint8 ndarray)."""
+    import numpy as np
+    ws = np.ascontiguousarray(ws, dtype=np.uint8).reshape(-1)
+    n = int(lib().q4_0_split_bytes(nrows, ncols_k))
+    if n < 0 or ws.size < n:
+        raise ValueError("invalid shape or weight buffer too small")
+    out = np.empty(n, np.uint8)
+    _check(lib().q4_0_from_split(ws.ctypes.data, out.ctypes.data, nrows, ncols_k), "q4_0_from_split")
+    return out
+
+
+def q4_0_to_split(w, out, nrows: int, ncols_k: int, stream=None) -> None:
+    """Device repack of block_q4_0 rows (w) into the split layout (out, 16-byte aligned)."""
+    n = nrows * (ncols_k // QK) * Q4_BLOCK_BYTES
+    if w.numel() * w.element_size() < n or out.numel() * out.element_size() < n:
+        raise ValueError("buffer too small")
+    _check(lib().q4_0_to_split_device(_dev(w, "w"), _dev(out, "out"), nrows, ncols_k, _stream(stream)),
+           "q4_0_to_split_device")
+
+
+def mat_mul_split(ws, xq, y, K: int, N: int, M: int, stream=None) -> None:
+    """y[M, N] = split-layout Q4_0 ws x Q8_1 xq (quantizer layout)."""
+    if ws.numel() * ws.element_size() < N * (K // QK) * Q4_BLOCK_BYTES:
+        raise ValueError("weight buffer too small")
+    if xq.numel() * xq.element_size() < M * (K // QSUPER) * Q8_BLOCK_BYTES or y.numel() < M * N:
+        raise ValueError("Q8_1 or output buffer too small")
+    _check(lib().mat_mul_q4_0s_q8_1_device(_dev(ws, "w"), _dev(xq, "xq"), _dev(y, "y"), K, N, M, _stream(stream)),
+           "mat_mul_q4_0s_q8_1_device")
+
+
+def mat_mul_split_f32(ws, x, xq, y, K: int, N: int, M: int, stream=None) -> None:
+    """Quantize fp32 x [M, K] (into xq, may be None when M == 1) and y = split W . x."""
+    import torch
+    if x.dtype != torch.float32 or y.dtype != torch.float32:
+        raise ValueError("x and y must be float32")
+    if x.numel() < M * K or y.numel() < M * N:
+        raise ValueError("x or y too small")
+    if xq is not None and xq.numel() * xq.element_size() < M * (K // QSUPER) * Q8_BLOCK_BYTES:
+        raise ValueError("Q8_1 workspace too small")
+    if ws.numel() * ws.element_size() < N * (K // QK) * Q4_BLOCK_BYTES:
+        raise ValueError("weight buffer too small")
+    xqp = _dev(xq, "xq") if xq is not None else ctypes.c_void_p(0)
+    _check(lib().mat_mul_q4_0s_q8_1_f32_device(_dev(ws, "w"), _dev(x, "x"), xqp, _dev(y, "y"), K, N, M,
+                                               _stream(stream)), "mat_mul_q4_0s_q8_1_f32_device")
 
 
 def block_sums(w, xq, out, K: int, N: int, M: int, stream=None) -> None:

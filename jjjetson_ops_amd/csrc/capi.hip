@@ -380,6 +380,72 @@ int mat_mul_q4_0_q8_1_f32_device(const void *d_w_q4_0, const float *d_x, void *d
     return run_mm(d_w_q4_0, d_quant_workspace, d_y, ncols_k, nrows_out, batch, JJO_ALGO_AUTO, s);
 }
 
+int q4_0_to_split_device(const void *d_w_q4_0, void *d_w_split, int nrows, int ncols_k, void *stream) {
+    clear_error();
+    if (d_w_q4_0 == nullptr || d_w_split == nullptr || d_w_q4_0 == d_w_split)
+        return set_error(JJO_ERR_INVALID_ARG, "q4_0_to_split_device: null or aliased buffers");
+    if (nrows <= 0 || ncols_k <= 0 || ncols_k % kQK != 0)
+        return set_error(JJO_ERR_INVALID_ARG, "q4_0_to_split_device: nrows=%d ncols_k=%d (ncols_k %% 32 == 0)", nrows,
+                         ncols_k);
+    if (!aligned(d_w_q4_0, 2) || !aligned(d_w_split, 16))
+        return set_error(JJO_ERR_INVALID_ARG, "q4_0_to_split_device: source 2-byte, destination 16-byte aligned");
+    const int64_t n = (int64_t)nrows * (ncols_k / kQK);
+    if ((n + 255) / 256 > 0x7fffffffLL) return set_error(JJO_ERR_INVALID_ARG, "q4_0_to_split_device: too large");
+    int rc = require_gfx950();
+    if (rc != JJO_OK) return rc;
+    hipError_t e = launch_q4_0_to_split(d_w_q4_0, d_w_split, n, (hipStream_t)stream);
+    return e == hipSuccess ? JJO_OK : hip_fail(e, "q4_0_to_split launch");
+}
+
+namespace {
+// Split-layout matmul from Q8_1 blocks (shapes validated by the caller).
+int run_mm_split(const void *w, const void *xq, float *y, int K, int N, int M, hipStream_t s) {
+    if (M > kGemvMaxBatch || K > kGemvMaxK || (int64_t)M * (K / kQK) * 48 > 150 * 1024)
+        return set_error(JJO_ERR_INVALID_ARG,
+                         "split-layout matmul supports batch <= %d and ncols_k <= %d with batch*ncols_k/32*48 <= "
+                         "150 KiB (got batch=%d ncols_k=%d)", kGemvMaxBatch, kGemvMaxK, M, K);
+    hipError_t e = launch_gemv_q4s(w, xq, y, K, N, M, s);
+    return e == hipSuccess ? JJO_OK : hip_fail(e, "gemv_q4s launch");
+}
+
+int validate_split(const void *w, const void *xq, const void *y, int K, int N, int M) {
+    int rc = validate_mm(w, xq, y, K, N, M);
+    if (rc != JJO_OK) return rc;
+    if (!aligned(w, 16)) return set_error(JJO_ERR_INVALID_ARG, "split-layout weight pointer must be 16-byte aligned");
+    return JJO_OK;
+}
+}  // namespace
+
+int mat_mul_q4_0s_q8_1_device(const void *d_w_split, const void *d_x_q8_1, float *d_y, int ncols_k, int nrows_out,
+                              int batch, void *stream) {
+    clear_error();
+    int rc = validate_split(d_w_split, d_x_q8_1, d_y, ncols_k, nrows_out, batch);
+    if (rc != JJO_OK) return rc;
+    if ((rc = require_gfx950()) != JJO_OK) return rc;
+    return run_mm_split(d_w_split, d_x_q8_1, d_y, ncols_k, nrows_out, batch, (hipStream_t)stream);
+}
+
+int mat_mul_q4_0s_q8_1_f32_device(const void *d_w_split, const float *d_x, void *d_quant_workspace, float *d_y,
+                                  int ncols_k, int nrows_out, int batch, void *stream) {
+    clear_error();
+    const void *xq_check = d_quant_workspace != nullptr ? d_quant_workspace : (const void *)d_x;
+    int rc = validate_split(d_w_split, xq_check, d_y, ncols_k, nrows_out, batch);
+    if (rc != JJO_OK) return rc;
+    if (d_x == nullptr || !aligned(d_x, 16))
+        return set_error(JJO_ERR_INVALID_ARG, "activation pointer must be non-null and 16-byte aligned");
+    if ((rc = require_gfx950()) != JJO_OK) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    if (batch == 1 && ncols_k <= kGemvMaxK) {
+        hipError_t e = launch_gemv_q4s_fused(d_w_split, d_x, d_quant_workspace, d_y, ncols_k, nrows_out, s);
+        return e == hipSuccess ? JJO_OK : hip_fail(e, "fused quantize+GEMV (split layout) launch");
+    }
+    if (d_quant_workspace == nullptr)
+        return set_error(JJO_ERR_INVALID_ARG, "quant workspace is required when batch > 1");
+    hipError_t e = launch_quantize_q8_1(d_x, d_quant_workspace, ncols_k, batch, 1, s);
+    if (e != hipSuccess) return hip_fail(e, "quantize_q8_1 launch");
+    return run_mm_split(d_w_split, d_quant_workspace, d_y, ncols_k, nrows_out, batch, s);
+}
+
 int mat_mul_q4_0_q8_1_block_sums_device(const void *d_w_q4_0, const void *d_x_q8_1, int32_t *d_sumi,
                                         int ncols_k, int nrows_out, int batch, void *stream) {
     clear_error();
@@ -537,8 +603,16 @@ int scratch_address(void **out) {
     if ((int)g_scratch_ptr.size() <= dev) g_scratch_ptr.resize(dev + 1, nullptr);
     if (g_scratch_ptr[dev] == nullptr) {
         void *p = nullptr;
+        // The first call may come while the caller's stream is being captured into a
+        // graph: the lookup enqueues nothing, so this thread's capture mode is
+        // relaxed around it (a global-mode capture would otherwise reject the call).
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        e = hipThreadExchangeStreamCaptureMode(&mode);
+        if (e != hipSuccess) return hip_fail(e, "hipThreadExchangeStreamCaptureMode");
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        hipError_t e2 = hipThreadExchangeStreamCaptureMode(&mode);
         if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (e2 != hipSuccess) return hip_fail(e2, "hipThreadExchangeStreamCaptureMode");
         if (p == nullptr) return set_error(JJO_ERR_HIP, "hipGetSymbolAddress(scratch) returned NULL");
         g_scratch_ptr[dev] = p;
     }
@@ -570,9 +644,11 @@ int linear_q4_0_forward_device_noalloc(void *stream, const float *input, const v
                          num_tokens, in_features, (long long)need, (long long)kNoAllocScratchBytes);
     int rc = require_gfx950();
     if (rc != JJO_OK) return rc;
-    // The decode step (one token) quantizes inside its GEMV and needs no scratch.
+    // A one-token step with in_features <= kGemvMaxK quantizes inside its GEMV and
+    // needs no scratch; every other call (a batch, or one token over a longer row)
+    // quantizes into the static buffer first.
     void *ws = nullptr;
-    if (num_tokens > 1 && (rc = scratch_address(&ws)) != JJO_OK) return rc;
+    if ((num_tokens > 1 || in_features > kGemvMaxK) && (rc = scratch_address(&ws)) != JJO_OK) return rc;
     return mat_mul_q4_0_q8_1_f32_device(weight_q4_0, input, ws, output, in_features, out_features, num_tokens,
                                         stream);
 }

@@ -428,6 +428,225 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
     }
 }
 
+// ---- split weight layout (nibble plane + fp16 scale plane) ----
+// Row n's block b: 16 nibble bytes at qs + (n*nb + b)*16 (the block_q4_0 qs bytes,
+// unchanged) and its fp16 scale at d + (n*nb + b)*2, with d = qs + N*nb*16.  Every
+// block is 16-byte aligned, so lane l of a wave reads block base + l of a row with
+// one 16-byte load: each load instruction of a wave covers one contiguous 1 KB run.
+// The activation record per (token, block) is 48 bytes in LDS: HI planes (16), LO
+// planes (16), d_x and -8*s_x (8), 8 bytes of padding so that consecutive lanes'
+// 16-byte reads hit disjoint banks.
+constexpr int kRecS = 48;
+
+__device__ __forceinline__ void put_block_s(uint8_t *rec, const uint32_t hi[4], const uint32_t lo[4], float dx,
+                                            float c) {
+    *reinterpret_cast<u32x4a16 *>(rec) = u32x4a16{hi[0], hi[1], hi[2], hi[3]};
+    *reinterpret_cast<u32x4a16 *>(rec + 16) = u32x4a16{lo[0], lo[1], lo[2], lo[3]};
+    *reinterpret_cast<u32x2a8 *>(rec + 32) = u32x2a8{__float_as_uint(dx), __float_as_uint(c)};
+}
+
+// Q8_1 item (token m, block b) -> record m*nb + b (items past the end: the spare).
+__device__ __forceinline__ void finish_q8_s(uint8_t *xs, const ItemQ8 &it, int item, int nb, int n_items) {
+    uint32_t hi[4], lo[4];
+    make_planes(it.q, hi, lo);
+    const size_t rec = item < n_items ? (size_t)item : (size_t)n_items;
+    put_block_s(xs + rec * kRecS, hi, lo, half_lo(it.ds), -8.0f * half_hi(it.ds));
+}
+
+// Fused staging for the split layout: the arithmetic of finish_f32 (the reference
+// quantizer's), written as per-block records.
+__device__ __forceinline__ void finish_f32_s(uint8_t *xs, uint8_t *__restrict__ xq_out, const ItemF32 &it,
+                                             int item, int nb, bool live) {
+    const int b = min(item >> 1, nb - 1), h = item & 1;
+    const f32x4 *v = it.v;
+    float am[4], su[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        am[i] = fmaxf(fabsf(v[i].x), fmaxf(fabsf(v[i].y), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+        float s = v[i].x + v[i].y;
+        s = s + v[i].z;
+        su[i] = s + v[i].w;
+    }
+    const float s0 = su[0] + su[2], s1 = su[1] + su[3];
+    const float m0 = fmaxf(am[0], am[2]), m1 = fmaxf(am[1], am[3]);
+    const float s0o = dpp<0xB1>(s0), s1o = dpp<0xB1>(s1);
+    const float m0o = dpp<0xB1>(m0), m1o = dpp<0xB1>(m1);
+    const float sum = (s0 + s0o) + (s1 + s1o);
+    const float amax = fmaxf(fmaxf(m0, m0o), fmaxf(m1, m1o));
+    const float d_inv = (amax > 0.0f) ? 127.0f / amax : 0.0f;
+    uint32_t q[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma clang fp contract(off)
+        const int32_t a = round_away(v[i].x * d_inv), bb = round_away(v[i].y * d_inv);
+        const int32_t c = round_away(v[i].z * d_inv), d = round_away(v[i].w * d_inv);
+        q[i] = (uint32_t)(a & 0xff) | ((uint32_t)(bb & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+               ((uint32_t)(d & 0xff) << 24);
+    }
+    if (!live) return;
+    uint8_t *rec = xs + (size_t)b * kRecS;
+    uint32_t hw[2], lw[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t a = q[i] ^ 0x80808080u;
+        const uint32_t bq = q[2 + i] ^ 0x80808080u;
+        lw[i] = (a & 0x0f0f0f0fu) | ((bq & 0x0f0f0f0fu) << 4);
+        hw[i] = ((a >> 4) & 0x0f0f0f0fu) | (bq & 0xf0f0f0f0u);
+    }
+    *reinterpret_cast<u32x2a8 *>(rec + 8 * h) = u32x2a8{hw[0], hw[1]};
+    *reinterpret_cast<u32x2a8 *>(rec + 16 + 8 * h) = u32x2a8{lw[0], lw[1]};
+    const __half hd = __float2half_rn(1.0f / d_inv);
+    const __half hs = __float2half_rn(sum);
+    if (h == 0)
+        *reinterpret_cast<u32x2a8 *>(rec + 32) =
+            u32x2a8{__float_as_uint(__half2float(hd)), __float_as_uint(-8.0f * __half2float(hs))};
+    if (xq_out != nullptr) {
+        uint8_t *blk = xq_out + (size_t)(b >> 2) * kQ8BlockBytes;
+        const int g = b & 3;
+        *reinterpret_cast<u32x2a8 *>(blk + 16 + 32 * g + 8 * h) = u32x2a8{q[0], q[1]};
+        *reinterpret_cast<u32x2a8 *>(blk + 16 + 32 * g + 16 + 8 * h) = u32x2a8{q[2], q[3]};
+        if (h == 0)
+            *reinterpret_cast<uint32_t *>(blk + 4 * g) =
+                (uint32_t)__half_as_ushort(hd) | ((uint32_t)__half_as_ushort(hs) << 16);
+    }
+}
+
+// Split-layout GEMV.  Workgroup = RG row groups x JS K-slices of 128 blocks (one
+// wave each, JS = ceil(K / 4096)); lane l of slice js owns blocks 128*js + l and
+// 128*js + 64 + l of its wave's U rows.  Each of those blocks is one nontemporal
+// 16-byte load (plus a 2-byte scale load); the integer dot is the dot8 plane form
+// of gemv_q4_0_q8_1_kernel.
+template <int M, int U, int JS, int RG, bool FUSED, int EARLY>
+__global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *__restrict__ w,
+                                                                const void *__restrict__ xin,
+                                                                uint8_t *__restrict__ xq_out,
+                                                                float *__restrict__ y, int K, int N) {
+    extern __shared__ __align__(16) uint8_t xs[];  // M * K/32 records of kRecS bytes + 1 spare
+    __shared__ float part[JS > 1 ? RG * JS * U * M : 1];
+
+    constexpr int kThreadsWG = 64 * JS * RG;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int js = wave % JS;
+    const int rg = wave / JS;
+    const int nb = K / kQK;
+    const int bk0 = 128 * js + lane;       // this lane's two blocks
+    const int bk1 = bk0 + 64;
+    const int c0 = min(bk0, nb - 1), c1 = min(bk1, nb - 1);
+    const uint16_t *__restrict__ dpl = reinterpret_cast<const uint16_t *>(w + (size_t)N * nb * 16);
+    const int r0 = (blockIdx.x * RG + rg) * U;
+    const int n_items = FUSED ? 2 * nb : M * nb;
+    const int rounds = (n_items + kThreadsWG - 1) / kThreadsWG;
+
+    // 1) activation requests (L2-resident), ahead of the weights
+    using Item = typename std::conditional<FUSED, ItemF32, ItemQ8>::type;
+    Item early[EARLY];
+#pragma unroll
+    for (int r = 0; r < EARLY; ++r) {
+        const int item = threadIdx.x + r * kThreadsWG;
+        if constexpr (FUSED) {
+            issue_f32(early[r], reinterpret_cast<const float *>(xin), item, nb);
+        } else {
+            issue_q8<M>(early[r], reinterpret_cast<const uint8_t *>(xin), item, nb);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // 2) weight requests: per row, two coalesced 16-byte nibble loads and two scales
+    u32x4a16 wq[U][2];
+    uint32_t wd[U][2];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const size_t base = (size_t)min(r0 + u, N - 1) * nb;
+        wq[u][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4a16 *>(w + (base + c0) * 16));
+        wq[u][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4a16 *>(w + (base + c1) * 16));
+        wd[u][0] = dpl[base + c0];
+        wd[u][1] = dpl[base + c1];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // 3) activation records of the whole K range in LDS, once per workgroup
+    uint8_t *xq_w = (FUSED && blockIdx.x == 0) ? xq_out : nullptr;
+#pragma unroll
+    for (int r = 0; r < EARLY; ++r) {
+        const int item = threadIdx.x + r * kThreadsWG;
+        if constexpr (FUSED) {
+            finish_f32_s(xs, xq_w, early[r], item, nb, item < n_items);
+        } else {
+            finish_q8_s(xs, early[r], item, nb, n_items);
+        }
+    }
+    for (int r = EARLY; r < rounds; ++r) {
+        const int item = threadIdx.x + r * kThreadsWG;
+        Item it;
+        if constexpr (FUSED) {
+            issue_f32(it, reinterpret_cast<const float *>(xin), item, nb);
+            finish_f32_s(xs, xq_w, it, item, nb, item < n_items);
+        } else {
+            issue_q8<M>(it, reinterpret_cast<const uint8_t *>(xin), item, nb);
+            finish_q8_s(xs, it, item, nb, n_items);
+        }
+    }
+    __syncthreads();
+
+    // 4) rows in load order
+    float acc[U][M];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[u][m] = 0.0f;
+
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const bool live = (k ? bk1 : bk0) < nb;
+            const int cb = k ? c1 : c0;
+            const uint32_t q[4] = {wq[u][k].x, wq[u][k].y, wq[u][k].z, wq[u][k].w};
+            const int32_t ns = nib_sum128(q);
+            const float dw = __half2float(__ushort_as_half((unsigned short)wd[u][k]));
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const uint8_t *rec = xs + ((size_t)m * nb + cb) * kRecS;
+                const u32x4a16 h4 = *reinterpret_cast<const u32x4a16 *>(rec);
+                const u32x4a16 l4 = *reinterpret_cast<const u32x4a16 *>(rec + 16);
+                const u32x2a8 c2 = *reinterpret_cast<const u32x2a8 *>(rec + 32);
+                const uint32_t hi[4] = {h4.x, h4.y, h4.z, h4.w}, lo[4] = {l4.x, l4.y, l4.z, l4.w};
+                const int32_t sv = block_sumi(q, hi, lo, ns);
+                const float v = dw * fmaf((float)sv, __uint_as_float(c2.x), __uint_as_float(c2.y));
+                acc[u][m] += live ? v : 0.0f;
+            }
+        }
+    }
+
+    constexpr int NV = pow2_at_least(U * M);
+    float v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] = i < U * M ? acc[i / M][i % M] : 0.0f;
+    const float s = multi_sum<NV>(v, lane);
+    const int idx = multi_sum_index<NV>(lane);
+    const int u = idx / M, m = idx % M;
+    const bool owner = (lane & (64 / NV - 1)) == 0 && idx < U * M;
+    if constexpr (JS == 1) {
+        if (owner && r0 + u < N) y[(size_t)m * N + r0 + u] = s;
+    } else {
+        if (owner) part[((rg * U + u) * M + m) * JS + js] = s;
+        __syncthreads();
+        if (js == 0) {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    if (lane == ((u * M + m) & 63) && r0 + u < N) {
+                        const float *pp = part + ((rg * U + u) * M + m) * JS;
+                        float s = pp[0];
+#pragma unroll
+                        for (int j = 1; j < JS; ++j) s += pp[j];
+                        y[(size_t)m * N + r0 + u] = s;
+                    }
+                }
+        }
+    }
+}
+
 // Row groups per workgroup (the activation staging of a workgroup is shared by
 // its RG row groups of U rows).  Single-token decode favours wide workgroups of
 // short row groups; multi-token batches favour four row groups of four rows.
@@ -449,40 +668,61 @@ constexpr int rg_for() {
     return JS == 1 ? kRgM : JS == 2 ? 2 : 1;
 }
 
-template <int M, int U, int JS, bool FUSED, int EARLY>
+// Split layout: row groups per workgroup.
+#ifndef JJO_Q4S_RG1F
+#define JJO_Q4S_RG1F 4
+#endif
+#ifndef JJO_Q4S_RG1
+#define JJO_Q4S_RG1 4
+#endif
+template <int M, int JS, bool FUSED = false>
+constexpr int rg_for_s() {
+    if (M == 1 && FUSED && JS == 1) return JJO_Q4S_RG1F;
+    if (M == 1) return JS == 1 ? JJO_Q4S_RG1 : JS == 2 ? 4 : JS == 3 ? 4 : 2;
+    return JS == 1 ? kRgM : JS == 2 ? 2 : 1;
+}
+
+template <bool SPLIT, int M, int U, int JS, bool FUSED, int EARLY>
 hipError_t launch_cfg(const void *w, const void *xin, uint8_t *xq_out, float *y, int K, int N, hipStream_t stream) {
-    constexpr int RG = rg_for<M, JS, FUSED>();
+    constexpr int RG = SPLIT ? rg_for_s<M, JS, FUSED>() : rg_for<M, JS, FUSED>();
     const int groups = (N + U - 1) / U;
     const int blocks = (groups + RG - 1) / RG;
-    const size_t smem = ((size_t)M * (K / 64) + 1) * kRec;
+    const size_t smem = SPLIT ? ((size_t)M * (K / 32) + 1) * kRecS : ((size_t)M * (K / 64) + 1) * kRec;
+    const void *kern = SPLIT ? (const void *)gemv_q4s_kernel<M, U, JS, RG, FUSED, EARLY>
+                             : (const void *)gemv_q4_0_q8_1_kernel<M, U, JS, RG, FUSED, EARLY>;
     if (smem > 64 * 1024) {
         // Raise this instantiation's dynamic-LDS limit to what the call needs.
-        hipError_t e = ensure_dynamic_lds((const void *)gemv_q4_0_q8_1_kernel<M, U, JS, RG, FUSED, EARLY>, smem);
+        hipError_t e = ensure_dynamic_lds(kern, smem);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL((gemv_q4_0_q8_1_kernel<M, U, JS, RG, FUSED, EARLY>), dim3(blocks), dim3(64 * JS * RG), smem,
-                       stream, (const uint8_t *)w, xin, xq_out, y, K, N);
+    if constexpr (SPLIT) {
+        hipLaunchKernelGGL((gemv_q4s_kernel<M, U, JS, RG, FUSED, EARLY>), dim3(blocks), dim3(64 * JS * RG), smem,
+                           stream, (const uint8_t *)w, xin, xq_out, y, K, N);
+    } else {
+        hipLaunchKernelGGL((gemv_q4_0_q8_1_kernel<M, U, JS, RG, FUSED, EARLY>), dim3(blocks), dim3(64 * JS * RG),
+                           smem, stream, (const uint8_t *)w, xin, xq_out, y, K, N);
+    }
     return hipGetLastError();
 }
 
-template <int M, int U, int JS, bool FUSED>
+template <bool SPLIT, int M, int U, int JS, bool FUSED>
 hipError_t launch_js(const void *w, const void *xin, uint8_t *xq_out, float *y, int K, int N, hipStream_t stream) {
-    constexpr int RG = rg_for<M, JS, FUSED>();
+    constexpr int RG = SPLIT ? rg_for_s<M, JS, FUSED>() : rg_for<M, JS, FUSED>();
     const int n_items = FUSED ? 2 * (K / kQK) : M * (K / kQK);
     const int rounds = (n_items + 64 * JS * RG - 1) / (64 * JS * RG);
-    if (rounds <= 1) return launch_cfg<M, U, JS, FUSED, 1>(w, xin, xq_out, y, K, N, stream);
-    if (rounds <= 2) return launch_cfg<M, U, JS, FUSED, 2>(w, xin, xq_out, y, K, N, stream);
-    return launch_cfg<M, U, JS, FUSED, 4>(w, xin, xq_out, y, K, N, stream);
+    if (rounds <= 1) return launch_cfg<SPLIT, M, U, JS, FUSED, 1>(w, xin, xq_out, y, K, N, stream);
+    if (rounds <= 2) return launch_cfg<SPLIT, M, U, JS, FUSED, 2>(w, xin, xq_out, y, K, N, stream);
+    return launch_cfg<SPLIT, M, U, JS, FUSED, 4>(w, xin, xq_out, y, K, N, stream);
 }
 
-template <int M, int U, bool FUSED>
+template <bool SPLIT, int M, int U, bool FUSED>
 hipError_t launch_m(const void *w, const void *xin, uint8_t *xq_out, float *y, int K, int N, hipStream_t stream) {
     const int js = (K / 64 + 63) / 64;
     switch (js) {
-        case 1: return launch_js<M, U, 1, FUSED>(w, xin, xq_out, y, K, N, stream);
-        case 2: return launch_js<M, U, 2, FUSED>(w, xin, xq_out, y, K, N, stream);
-        case 3: return launch_js<M, U, 3, FUSED>(w, xin, xq_out, y, K, N, stream);
-        case 4: return launch_js<M, U, 4, FUSED>(w, xin, xq_out, y, K, N, stream);
+        case 1: return launch_js<SPLIT, M, U, 1, FUSED>(w, xin, xq_out, y, K, N, stream);
+        case 2: return launch_js<SPLIT, M, U, 2, FUSED>(w, xin, xq_out, y, K, N, stream);
+        case 3: return launch_js<SPLIT, M, U, 3, FUSED>(w, xin, xq_out, y, K, N, stream);
+        case 4: return launch_js<SPLIT, M, U, 4, FUSED>(w, xin, xq_out, y, K, N, stream);
         default: return hipErrorInvalidValue;  // K > 16384: the C ABI routes these to the MFMA GEMM
     }
 }
@@ -493,21 +733,47 @@ hipError_t launch_m(const void *w, const void *xin, uint8_t *xq_out, float *y, i
 hipError_t launch_gemv_dot4(const void *w, const void *xq, float *y, int K, int N, int M,
                             hipStream_t stream) {
     switch (M) {
-        case 1: return launch_m<1, kU1, false>(w, xq, nullptr, y, K, N, stream);
-        case 2: return launch_m<2, 2, false>(w, xq, nullptr, y, K, N, stream);
-        case 3: return launch_m<3, 4, false>(w, xq, nullptr, y, K, N, stream);
-        case 4: return launch_m<4, kU4, false>(w, xq, nullptr, y, K, N, stream);
-        case 5: return launch_m<5, 2, false>(w, xq, nullptr, y, K, N, stream);
-        case 6: return launch_m<6, 2, false>(w, xq, nullptr, y, K, N, stream);
-        case 7: return launch_m<7, 2, false>(w, xq, nullptr, y, K, N, stream);
-        case 8: return launch_m<8, 2, false>(w, xq, nullptr, y, K, N, stream);
+        case 1: return launch_m<false, 1, kU1, false>(w, xq, nullptr, y, K, N, stream);
+        case 2: return launch_m<false, 2, 2, false>(w, xq, nullptr, y, K, N, stream);
+        case 3: return launch_m<false, 3, 4, false>(w, xq, nullptr, y, K, N, stream);
+        case 4: return launch_m<false, 4, kU4, false>(w, xq, nullptr, y, K, N, stream);
+        case 5: return launch_m<false, 5, 2, false>(w, xq, nullptr, y, K, N, stream);
+        case 6: return launch_m<false, 6, 2, false>(w, xq, nullptr, y, K, N, stream);
+        case 7: return launch_m<false, 7, 2, false>(w, xq, nullptr, y, K, N, stream);
+        case 8: return launch_m<false, 8, 2, false>(w, xq, nullptr, y, K, N, stream);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_gemv_fused(const void *w, const float *x, void *xq_out, float *y, int K, int N,
                              hipStream_t stream) {
-    return launch_m<1, kU1F, true>(w, x, (uint8_t *)xq_out, y, K, N, stream);
+    return launch_m<false, 1, kU1F, true>(w, x, (uint8_t *)xq_out, y, K, N, stream);
+}
+
+#ifndef JJO_Q4S_U1
+#define JJO_Q4S_U1 4
+#endif
+#ifndef JJO_Q4S_U1F
+#define JJO_Q4S_U1F 4
+#endif
+
+hipError_t launch_gemv_q4s(const void *w, const void *xq, float *y, int K, int N, int M, hipStream_t stream) {
+    switch (M) {
+        case 1: return launch_m<true, 1, JJO_Q4S_U1, false>(w, xq, nullptr, y, K, N, stream);
+        case 2: return launch_m<true, 2, 2, false>(w, xq, nullptr, y, K, N, stream);
+        case 3: return launch_m<true, 3, 4, false>(w, xq, nullptr, y, K, N, stream);
+        case 4: return launch_m<true, 4, 4, false>(w, xq, nullptr, y, K, N, stream);
+        case 5: return launch_m<true, 5, 2, false>(w, xq, nullptr, y, K, N, stream);
+        case 6: return launch_m<true, 6, 2, false>(w, xq, nullptr, y, K, N, stream);
+        case 7: return launch_m<true, 7, 2, false>(w, xq, nullptr, y, K, N, stream);
+        case 8: return launch_m<true, 8, 2, false>(w, xq, nullptr, y, K, N, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_gemv_q4s_fused(const void *w, const float *x, void *xq_out, float *y, int K, int N,
+                                 hipStream_t stream) {
+    return launch_m<true, 1, JJO_Q4S_U1F, true>(w, x, (uint8_t *)xq_out, y, K, N, stream);
 }
 
 }  // namespace jjo

@@ -42,6 +42,13 @@ hipError_t launch_gemv_dot4(const void *w, const void *xq, float *y, int K, int 
 // launch_quantize_q8_1); xq_out (nullable) receives the Q8_1 bytes.
 hipError_t launch_gemv_fused(const void *w, const float *x, void *xq_out, float *y, int K, int N,
                              hipStream_t stream);
+// Split weight layout (nibble plane + fp16 scale plane): GEMV at batch <= 8 from
+// Q8_1 input, and the fused quantize + GEMV at batch 1.
+hipError_t launch_gemv_q4s(const void *w, const void *xq, float *y, int K, int N, int M, hipStream_t stream);
+hipError_t launch_gemv_q4s_fused(const void *w, const float *x, void *xq_out, float *y, int K, int N,
+                                 hipStream_t stream);
+// block_q4_0 rows -> split layout (n_blocks blocks; out must not alias w).
+hipError_t launch_q4_0_to_split(const void *w, void *out, int64_t n_blocks, hipStream_t stream);
 // Batch <= 32: int8 MFMA 16x16 tiles, weights streamed per wave, K split over 4 waves.
 bool gemm_skinny_supported(const void *w, const void *xq, int K, int M);
 hipError_t launch_gemm_skinny(const void *w, const void *xq, float *y, int K, int N, int M,

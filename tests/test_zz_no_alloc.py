@@ -9,7 +9,9 @@ if __name__ == "__main__":  # `python tests/<file>.py`, as the reference runs it
     import pytest as _pytest
     _sys.exit(_pytest.main([__file__, "-q"]))
 import ctypes
+import subprocess
 import sys
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -51,7 +53,10 @@ def _no_alloc(x, w, K, N, T, dev):
 
 
 @pytest.mark.parametrize("K,N,T1,T2", [(4096, 1024, 300, 37), (1024, 4096, 64, 5), (4096, 14336, 16, 2),
-                                       (11008, 256, 3, 1)])
+                                       (11008, 256, 3, 1),
+                                       # one token over a row longer than the fused GEMV takes:
+                                       # the quantize goes through the static buffer
+                                       (20480, 192, 2, 1)])
 def test_no_alloc_matches_workspace_entry(K, N, T1, T2, dev):
     import torch
     rng = np.random.default_rng(K + T1)
@@ -90,3 +95,14 @@ def test_no_alloc_rejects_oversized_batch(dev):
     capi.linear_q4_0_noalloc(x2, w, y2, K, N, Tmax)
     torch.cuda.synchronize()
     assert bool(torch.isfinite(y2).all())
+
+
+def test_no_alloc_first_call_under_graph_capture():
+    """In a fresh process, the entry's first call on the device (which resolves the
+    static buffer's address) is made while the stream is captured into a HIP graph;
+    every replay must equal the workspace entry bit for bit."""
+    script = Path(__file__).resolve().parent / "gpu_scripts" / "no_alloc_graph.py"
+    note("no-alloc linear: first call inside graph capture (fresh process)")
+    r = subprocess.run([sys.executable, str(script)], capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-3000:]
+    assert r.stdout.strip().endswith("ok"), r.stdout[-2000:]
