@@ -444,6 +444,8 @@ def main():
         ("m16_k4096_n14336", 16, 4096, 14336, 2, args.steps),
         ("prefill_m2048_k4096_n4096", 2048, 4096, 4096, 3, max(20, args.steps // 4)),
         ("prefill_m2048_k4096_n14336", 2048, 4096, 14336, 3, max(20, args.steps // 4)),
+        ("prefill_m2048_k4096_n4096_split", 2048, 4096, 4096, 3, max(20, args.steps // 4)),
+        ("prefill_m2048_k4096_n14336_split", 2048, 4096, 14336, 3, max(20, args.steps // 4)),
         # A short prompt's prefill (the small-tile GEMM range), beside the headline configs.
         ("prefill_m128_k4096_n14336", 128, 4096, 14336, 3, max(20, args.steps // 4)),
     ]

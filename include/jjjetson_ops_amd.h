@@ -141,9 +141,9 @@ int q4_0_to_split_device(const void *d_w_q4_0, void *d_w_split, int nrows, int n
 
 /*
  * mat_mul_q4_0_q8_1_device (src/cuda/mm_q4_0_q8_1.cu:394, same arguments and
- * results) on a split-layout weight (16-byte aligned).  Batch <= 8 with
- * batch*ncols_k/32*48 <= 150 KiB and ncols_k <= 16384; other shapes return
- * JJO_ERR_INVALID_ARG.
+ * results) on a split-layout weight (16-byte aligned): the GEMV up to batch 8
+ * (ncols_k <= 16384, batch*ncols_k/32*48 <= 150 KiB), the int8-MFMA GEMM
+ * otherwise.
  */
 int mat_mul_q4_0s_q8_1_device(const void *d_w_split, const void *d_x_q8_1, float *d_y, int ncols_k,
                               int nrows_out, int batch, void *stream);
@@ -164,6 +164,7 @@ int mat_mul_q4_0s_q8_1_f32_device(const void *d_w_split, const float *d_x, void 
 #define JJO_ALGO_SKINNY_LDS 4 /* int8 MFMA 16x16 tiles, activation resident in LDS, batch <= 16 */
 #define JJO_ALGO_MFMA64 5     /* int8 MFMA GEMM with 64x64 workgroup tiles, any batch */
 #define JJO_ALGO_MFMA32 6     /* int8 MFMA GEMM with 32-row x 64-token workgroup tiles, any batch */
+#define JJO_ALGO_MFMA_W32 7   /* int8 MFMA GEMM, 128 x 128 tiles, one wave per 32 rows x 128 tokens */
 
 /*
  * As mat_mul_q4_0_q8_1_device with an explicit kernel choice.  Has no

@@ -24,7 +24,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 LIB = PKG / "libjjjetson_ops_amd.so"
 
 HIP_SOURCES = ["quantize_q8_1.hip", "gemv_q4_0_q8_1.hip", "gemm_skinny_q4_0_q8_1.hip", "gemm_skinny_persist.hip", "gemm_q4_0_q8_1_mfma.hip", "gemm_q4_0_q8_1_mfma64.hip", "moe_route.hip",
-               "quantize_q4_0.hip", "q4_0_split.hip", "weights_q4_0.cpp", "capi.hip"]
+               "quantize_q4_0.hip", "q4_0_split.hip", "gemm_q4s_mfma.hip", "weights_q4_0.cpp", "capi.hip"]
 HIP_FLAGS = [
     "--offload-arch=gfx950",
     "-O3",

@@ -25,6 +25,7 @@ ALGO_SKINNY = 3
 ALGO_SKINNY_LDS = 4
 ALGO_MFMA64 = 5
 ALGO_MFMA32 = 6
+ALGO_MFMA_W32 = 7
 
 QK = 32
 QSUPER = 128

@@ -213,6 +213,10 @@ int run_mm(const void *w, const void *xq, float *y, int K, int N, int M, int alg
         if ((M + 63) / 64 > 65535) return set_error(JJO_ERR_INVALID_ARG, "batch too large");
         e = launch_gemm_mfma64(w, xq, y, K, N, M, s, algo == JJO_ALGO_MFMA32 ? 32 : 64);
         if (e != hipSuccess) return hip_fail(e, "gemm_q4_0_q8_1_mfma64 launch");
+    } else if (algo == JJO_ALGO_MFMA_W32) {
+        if ((M + 127) / 128 > 65535) return set_error(JJO_ERR_INVALID_ARG, "batch too large");
+        e = launch_gemm_q4s_mfma(w, xq, y, K, N, M, false, s);
+        if (e != hipSuccess) return hip_fail(e, "gemm_q4s_mfma launch");
     } else if (algo == JJO_ALGO_MFMA) {
         if ((M + 127) / 128 > 65535) return set_error(JJO_ERR_INVALID_ARG, "batch too large");
         e = launch_gemm_mfma(w, xq, y, K, N, M, s);
@@ -260,6 +264,8 @@ __global__ __launch_bounds__(256) void read_floor_kernel(const uint4 *__restrict
 }
 
 }  // namespace
+
+int device_cu_count() { return device_cus(); }
 
 hipError_t launch_block_sums(const void *w, const void *xq, int32_t *sumi, int K, int N, int M,
                              hipStream_t stream) {
@@ -400,12 +406,12 @@ int q4_0_to_split_device(const void *d_w_q4_0, void *d_w_split, int nrows, int n
 namespace {
 // Split-layout matmul from Q8_1 blocks (shapes validated by the caller).
 int run_mm_split(const void *w, const void *xq, float *y, int K, int N, int M, hipStream_t s) {
-    if (M > kGemvMaxBatch || K > kGemvMaxK || (int64_t)M * (K / kQK) * 48 > 150 * 1024)
-        return set_error(JJO_ERR_INVALID_ARG,
-                         "split-layout matmul supports batch <= %d and ncols_k <= %d with batch*ncols_k/32*48 <= "
-                         "150 KiB (got batch=%d ncols_k=%d)", kGemvMaxBatch, kGemvMaxK, M, K);
-    hipError_t e = launch_gemv_q4s(w, xq, y, K, N, M, s);
-    return e == hipSuccess ? JJO_OK : hip_fail(e, "gemv_q4s launch");
+    if (M <= kGemvMaxBatch && K <= kGemvMaxK && (int64_t)M * (K / kQK) * 48 <= 150 * 1024) {
+        hipError_t e = launch_gemv_q4s(w, xq, y, K, N, M, s);
+        return e == hipSuccess ? JJO_OK : hip_fail(e, "gemv_q4s launch");
+    }
+    hipError_t e = launch_gemm_q4s_mfma(w, xq, y, K, N, M, true, s);
+    return e == hipSuccess ? JJO_OK : hip_fail(e, "gemm_q4s_mfma launch");
 }
 
 int validate_split(const void *w, const void *xq, const void *y, int K, int N, int M) {

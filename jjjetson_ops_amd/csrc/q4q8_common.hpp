@@ -32,6 +32,10 @@ int hip_fail(hipError_t e, const char *what);
 // thread-safely; later calls with the same or a smaller size cost a lookup.
 hipError_t ensure_dynamic_lds(const void *kernel, size_t bytes);
 
+// Compute units of the current device (256 on MI355X; the value found when the
+// C ABI checked the device).
+int device_cu_count();
+
 // Kernel launchers (asynchronous on `stream`).  Shapes are validated by the
 // C-ABI layer before these are called.
 hipError_t launch_quantize_q8_1(const float *x, void *y, int64_t K, int64_t ne1, int64_t nz,
@@ -47,6 +51,10 @@ hipError_t launch_gemv_fused(const void *w, const float *x, void *xq_out, float 
 hipError_t launch_gemv_q4s(const void *w, const void *xq, float *y, int K, int N, int M, hipStream_t stream);
 hipError_t launch_gemv_q4s_fused(const void *w, const float *x, void *xq_out, float *y, int K, int N,
                                  hipStream_t stream);
+// Int8-MFMA GEMM, one wave per 32 rows x 128 tokens; weights in the split layout
+// (split = true, 16-byte aligned) or block_q4_0 rows (4-byte aligned).
+hipError_t launch_gemm_q4s_mfma(const void *w, const void *xq, float *y, int K, int N, int M, bool split,
+                                hipStream_t stream);
 // block_q4_0 rows -> split layout (n_blocks blocks; out must not alias w).
 hipError_t launch_q4_0_to_split(const void *w, void *out, int64_t n_blocks, hipStream_t stream);
 // Batch <= 32: int8 MFMA 16x16 tiles, weights streamed per wave, K split over 4 waves.

@@ -151,7 +151,7 @@ def test_gemv(K, N, M, dev):
     (4096, 256, 128), (4096, 300, 130), (256, 128, 1), (640, 200, 16), (11008, 128, 64), (384, 64, 257),
     (1024, 70, 33), (512, 4100, 96), (128, 96, 70), (128, 5, 40),
 ])
-@pytest.mark.parametrize("algo", [capi.ALGO_MFMA, capi.ALGO_MFMA64, capi.ALGO_MFMA32])
+@pytest.mark.parametrize("algo", [capi.ALGO_MFMA, capi.ALGO_MFMA64, capi.ALGO_MFMA32, capi.ALGO_MFMA_W32])
 def test_gemm_mfma(K, N, M, algo, dev):
     note(f"gemm mfma algo={algo} K={K} N={N} M={M}")
     w = make_w(N, K, 3 * N + K)
@@ -292,7 +292,7 @@ def test_zero_activation_group_gives_nan_like_reference(dev):
     xq = c_oracle.quantize_q8_1(x, [K, M])
     exp = c_oracle.matmul(w, xq, K, N, M)
     assert np.all(np.isnan(exp[1])) and np.all(np.isfinite(exp[0]))
-    for algo in (capi.ALGO_GEMV, capi.ALGO_MFMA):
+    for algo in (capi.ALGO_GEMV, capi.ALGO_MFMA, capi.ALGO_MFMA_W32):
         got = run_mm(w, xq, K, N, M, algo, dev)
         assert np.all(np.isnan(got[1]))
         np.testing.assert_allclose(got[0], exp[0], rtol=RTOL, atol=ATOL)
@@ -316,7 +316,7 @@ def test_infinite_block_sum_gives_inf_like_reference(M, dev):
     xq = c_oracle.quantize_q8_1(x, [K, M])
     exp = c_oracle.matmul(w, xq, K, N, M)
     assert np.all(np.isinf(exp[1]))
-    algos = [capi.ALGO_MFMA, capi.ALGO_MFMA64, capi.ALGO_MFMA32] + ([capi.ALGO_GEMV] if M <= 8 else []) + ([capi.ALGO_SKINNY] if M <= 32 else [])
+    algos = [capi.ALGO_MFMA, capi.ALGO_MFMA64, capi.ALGO_MFMA32, capi.ALGO_MFMA_W32] + ([capi.ALGO_GEMV] if M <= 8 else []) + ([capi.ALGO_SKINNY] if M <= 32 else [])
     algos += [capi.ALGO_SKINNY_LDS] if M <= 16 else []
     for algo in algos:
         got = run_mm(w, xq, K, N, M, algo, dev)

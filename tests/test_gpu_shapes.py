@@ -47,7 +47,7 @@ def test_every_kernel_on_shape(K, N, M, dev):
     w_pad = torch.zeros(w.size + 16, dtype=torch.uint8, device=dev)
     w_pad[4:4 + w.size] = torch.from_numpy(w).to(dev)
     for algo in (capi.ALGO_AUTO, capi.ALGO_GEMV, capi.ALGO_SKINNY, capi.ALGO_SKINNY_LDS, capi.ALGO_MFMA,
-                 capi.ALGO_MFMA64, capi.ALGO_MFMA32):
+                 capi.ALGO_MFMA64, capi.ALGO_MFMA32, capi.ALGO_MFMA_W32):
         if not _accepts(algo, K, N, M):
             continue
         for off in (0, 4):
@@ -59,3 +59,20 @@ def test_every_kernel_on_shape(K, N, M, dev):
             torch.cuda.synchronize()
             np.testing.assert_allclose(y.cpu().numpy().reshape(M, N), exp, rtol=RTOL, atol=ATOL,
                                        err_msg=f"algo={algo} offset={off}")
+
+
+@pytest.mark.parametrize("K,N,M", SHAPES)
+def test_split_layout_on_shape(K, N, M, dev):
+    """The same shapes through the split weight layout (repacked on the device)."""
+    import torch
+    print(f"[case] split shapes K={K} N={N} M={M}", flush=True)
+    w = c_oracle.quantize_q4_0((np.random.default_rng(K * N + M).standard_normal((N, K)) * 0.02).astype(np.float32))
+    x = np.random.default_rng(M).standard_normal((M, K)).astype(np.float32)
+    xq = c_oracle.quantize_q8_1(x, [K, M])
+    exp = c_oracle.matmul(w, xq, K, N, M)
+    ws = torch.empty(w.size, dtype=torch.uint8, device=dev)
+    capi.q4_0_to_split(torch.from_numpy(w).to(dev), ws, N, K)
+    y = torch.full((M * N,), float("nan"), dtype=torch.float32, device=dev)
+    capi.mat_mul_split(ws, torch.from_numpy(xq).to(dev), y, K, N, M)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(y.cpu().numpy().reshape(M, N), exp, rtol=RTOL, atol=ATOL)

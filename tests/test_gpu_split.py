@@ -126,14 +126,51 @@ def test_split_f32_batch(M, dev):
     np.testing.assert_allclose(host(y).reshape(M, N), c_oracle.matmul(w, xq_ref, K, N, M), rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("K,N,M", [(4096, 256, 128), (4096, 300, 130), (384, 64, 257), (128, 96, 9),
+                                   (11008, 128, 64), (512, 4100, 96)])
+def test_split_gemm(K, N, M, dev):
+    import torch
+    note(f"split gemm M={M} K={K} N={N}")
+    rng = np.random.default_rng(K + 3 * N + M)
+    w = _weights(rng, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    xq = c_oracle.quantize_q8_1(x, [K, M])
+    ws = split_dev(w, N, K, dev)
+    y = torch.full((M * N,), float("nan"), dtype=torch.float32, device=dev)
+    capi.mat_mul_split(ws, to_dev(xq, dev), y, K, N, M)
+    np.testing.assert_allclose(host(y).reshape(M, N), c_oracle.matmul(w, xq, K, N, M), rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("K,N,M", [(256, 5120, 1700), (256, 14336, 2048), (128, 128 * 33, 128 * 16 + 5)])
+def test_split_gemm_tail_round(K, N, M, dev):
+    """Tile counts that leave a partial last round of at most half the 512 slots
+    (2 per CU): that round runs as 64-token half tiles, including a half that lies
+    entirely past M.  Checked on a row subset that includes both ends of every
+    128-row tile boundary touched."""
+    import torch
+    note(f"split gemm tail round M={M} K={K} N={N}")
+    rng = np.random.default_rng(K + N + M)
+    w = _weights(rng, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    xq = c_oracle.quantize_q8_1(x, [K, M])
+    ws = split_dev(w, N, K, dev)
+    y = torch.full((M * N,), float("nan"), dtype=torch.float32, device=dev)
+    capi.mat_mul_split(ws, to_dev(xq, dev), y, K, N, M)
+    got = host(y).reshape(M, N)
+    rows = np.unique(np.concatenate([rng.choice(N, 200, replace=False), [0, 127, 128, N - 129, N - 128, N - 1]]))
+    nb = K // 32
+    wsub = np.ascontiguousarray(w.reshape(N, nb * 18)[rows]).reshape(-1)
+    exp = c_oracle.matmul(wsub, xq, K, rows.size, M)
+    np.testing.assert_allclose(got[:, rows], exp, rtol=RTOL, atol=ATOL)
+    assert np.all(np.isfinite(got))
+
+
 def test_split_rejects_unsupported(dev):
     import torch
-    K, N, M = 4096, 64, 9
+    K, N, M = 4096, 64, 1
     ws = torch.zeros(N * (K // 32) * 18 + 16, dtype=torch.uint8, device=dev)
     xq = torch.zeros(capi.q8_1_output_bytes([K, M]), dtype=torch.uint8, device=dev)
     y = torch.full((M * N,), 5.0, dtype=torch.float32, device=dev)
-    with pytest.raises(RuntimeError, match="split-layout"):
-        capi.mat_mul_split(ws, xq, y, K, N, M)
     with pytest.raises(RuntimeError, match="16-byte aligned"):
-        capi.mat_mul_split(ws[4:], xq, y, K, N, 1)
+        capi.mat_mul_split(ws[4:], xq, y, K, N, M)
     assert bool((y == 5.0).all())
