@@ -221,7 +221,7 @@ def time_moe(dev, steps, warmup):
 def time_moe_ffn(dev, steps, warmup):
     """The whole Q4_0 MoE FFN of the same layer shape (8 experts, top-2, 512 tokens,
     H=4096, I=14336): quantize, top-k, dispatch, gate|up, SwiGLU+quantize, down,
-    combine -- eight launches per step."""
+    combine -- seven launches per step (gate|up, SwiGLU and its Q8_1 quantization are one)."""
     import torch
     from jjjetson_ops_amd import capi
 
@@ -240,7 +240,7 @@ def time_moe_ffn(dev, steps, warmup):
 
     for i in range(warmup):
         step(i)
-    avg = _time_steps(step, steps, 8) / steps
+    avg = _time_steps(step, steps, 7) / steps
     R = T * topk
     ops = 2.0 * R * 3 * I * H
     wbytes = 3 * E * I * (H // 32) * 18  # 792 MB: every step streams past the MALL
@@ -248,7 +248,7 @@ def time_moe_ffn(dev, steps, warmup):
     return {"name": "moe_ffn_q4_0_e8_top2_t512_h4096_i14336", "routes": R, "H": H, "I": I,
             "us_per_step": avg * 1e3, "TOPS": ops / (avg * 1e-3) / 1e12,
             "mfma_frac": ops / (avg * 1e-3) / 1e12 / INT8_PEAK_TOPS,
-            "weight_GBps": wbytes / (avg * 1e-3) / 1e9, "launches_per_step": 8}
+            "weight_GBps": wbytes / (avg * 1e-3) / 1e9, "launches_per_step": 7}
 
 def time_read_floor(dev, steps, warmup, nbytes=11008 * (4096 // 32) * 18):
     """The single-launch HBM read floor: one plain coalesced read of the decode GEMV's

@@ -300,6 +300,20 @@ int moe_q4_0_gate_up_device(void *stream, const void *w_gate, const void *w_up, 
                             int intermediate_size, int n_routes);
 
 /*
+ * The gate|up projection fused with SwiGLU and the Q8_1 quantization of its
+ * result, in one grouped launch: mid_q8_1 receives the Q8_1 bytes (quantizer
+ * layout over the R = n_routes permuted rows, intermediate_size values each) of
+ * silu(gate) * up, bit for bit what moe_q4_0_gate_up_device followed by
+ * swiglu_quantize_q8_1_device writes, with no fp32 [R][2I] buffer.  Replaces the
+ * gate/up moe_grouped_gemm_nt calls and swiglu_silu_mul_launch_cuda
+ * (src/cuda/moe/moe_pipeline_sota.cu:181-191, src/cuda/swiglu.cu:5-28).
+ * intermediate_size % 128 == 0.
+ */
+int moe_q4_0_gate_up_swiglu_q8_1_device(void *stream, const void *w_gate, const void *w_up,
+                                        const void *x_q8_1_permuted, const int32_t *expert_offsets, int num_experts,
+                                        void *mid_q8_1, int hidden_size, int intermediate_size, int n_routes);
+
+/*
  * SwiGLU fused with the Q8_1 quantizer: mid = silu(gate) * up
  * (swiglu_silu_mul_launch_device, src/cuda/swiglu.cu:5-28) on gate_up [rows][2I],
  * quantized to Q8_1 (quantizer layout over `rows` tokens, I values) for the down

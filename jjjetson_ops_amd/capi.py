@@ -55,6 +55,7 @@ EXPORTED_SYMBOLS = (
     "moe_top_k_device",
     "moe_dispatch_q8_1_device",
     "moe_q4_0_gate_up_device",
+    "moe_q4_0_gate_up_swiglu_q8_1_device",
     "swiglu_quantize_q8_1_device",
     "moe_combine_device",
     "moe_q4_0_ffn_workspace_bytes",
@@ -153,6 +154,8 @@ def lib() -> ctypes.CDLL:
         L.moe_dispatch_q8_1_device.argtypes = [vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp]
         L.moe_q4_0_gate_up_device.restype = i32
         L.moe_q4_0_gate_up_device.argtypes = [vp, vp, vp, vp, vp, i32, vp, i32, i32, i32]
+        L.moe_q4_0_gate_up_swiglu_q8_1_device.restype = i32
+        L.moe_q4_0_gate_up_swiglu_q8_1_device.argtypes = [vp, vp, vp, vp, vp, i32, vp, i32, i32, i32]
         L.swiglu_quantize_q8_1_device.restype = i32
         L.swiglu_quantize_q8_1_device.argtypes = [vp, vp, vp, vp, i32, i32]
         L.moe_combine_device.restype = i32
@@ -428,6 +431,14 @@ def moe_gate_up(w_gate, w_up, xq_perm, offsets, num_experts: int, gate_up, hidde
                                          _dev(xq_perm, "xq_perm"), _dev(offsets, "offsets"), num_experts,
                                          _dev(gate_up, "gate_up"), hidden, inter, n_routes),
            "moe_q4_0_gate_up_device")
+
+
+def moe_gate_up_swiglu(w_gate, w_up, xq_perm, offsets, num_experts: int, mid_q, hidden: int, inter: int,
+                       n_routes: int, stream=None) -> None:
+    _check(lib().moe_q4_0_gate_up_swiglu_q8_1_device(_stream(stream), _dev(w_gate, "w_gate"), _dev(w_up, "w_up"),
+                                                     _dev(xq_perm, "xq_perm"), _dev(offsets, "offsets"), num_experts,
+                                                     _dev(mid_q, "mid_q"), hidden, inter, n_routes),
+           "moe_q4_0_gate_up_swiglu_q8_1_device")
 
 
 def swiglu_quantize(gate_up, mid_q, rows: int, inter: int, mid_f32=None, stream=None) -> None:

@@ -721,7 +721,7 @@ struct MoeWs {
     float *route_w;
     int32_t *ids, *offsets, *src_route, *dst_of_route;
     uint8_t *xq, *xp, *midq;
-    float *gate_up, *eout;
+    float *eout;
     int64_t bytes;
 };
 
@@ -742,7 +742,6 @@ MoeWs moe_ws_layout(uint8_t *base, int T, int H, int I, int E, int top_k) {
     w.dst_of_route = (int32_t *)take(R * 4);
     w.xq = take((int64_t)T * (H / kQSuper) * kQ8BlockBytes);
     w.xp = take(R * (H / kQSuper) * kQ8BlockBytes);
-    w.gate_up = (float *)take(R * 2 * I * 4);
     w.midq = take(R * (I / kQSuper) * kQ8BlockBytes);
     w.eout = (float *)take(R * H * 4);
     w.bytes = off;
@@ -822,6 +821,25 @@ int moe_q4_0_gate_up_device(void *stream, const void *w_gate, const void *w_up, 
     return e == hipSuccess ? JJO_OK : hip_fail(e, "moe_gate_up launch");
 }
 
+int moe_q4_0_gate_up_swiglu_q8_1_device(void *stream, const void *w_gate, const void *w_up,
+                                        const void *x_q8_1_permuted, const int32_t *expert_offsets, int num_experts,
+                                        void *mid_q8_1, int hidden_size, int intermediate_size, int n_routes) {
+    clear_error();
+    int rc = validate_mm(w_gate, x_q8_1_permuted, mid_q8_1, hidden_size, 2 * intermediate_size, n_routes);
+    if (rc != JJO_OK) return rc;
+    if (w_up == nullptr || !aligned(w_up, 4) || expert_offsets == nullptr || num_experts <= 0 ||
+        num_experts > 4096)
+        return set_error(JJO_ERR_INVALID_ARG, "moe_gate_up_swiglu: bad w_up / expert_offsets / num_experts");
+    if (intermediate_size % 128 != 0)
+        return set_error(JJO_ERR_INVALID_ARG, "moe_gate_up_swiglu: intermediate_size must be a multiple of 128");
+    if ((rc = check_grouped_grid(n_routes, num_experts)) != JJO_OK) return rc;
+    if ((rc = require_gfx950()) != JJO_OK) return rc;
+    hipError_t e = launch_gemm_gate_up_swiglu_q8_1(w_gate, w_up, x_q8_1_permuted, expert_offsets, num_experts,
+                                                   mid_q8_1, hidden_size, intermediate_size, n_routes,
+                                                   (hipStream_t)stream);
+    return e == hipSuccess ? JJO_OK : hip_fail(e, "moe_gate_up_swiglu launch");
+}
+
 int moe_combine_device(void *stream, const float *expert_out, const int32_t *dst_of_route,
                        const float *route_weights, float *y, int num_tokens, int hidden_size, int top_k) {
     clear_error();
@@ -873,12 +891,10 @@ int moe_q4_0_ffn_forward_device(void *stream, const float *x, const float *logit
         return hip_fail(e, "moe_ffn dispatch");
     if ((e = launch_moe_gather_q8_1(ws.xq, ws.src_route, ws.xp, T, R, top_k, H, s)) != hipSuccess)
         return hip_fail(e, "moe_ffn gather");
-    // 4) gate|up of every route's expert in one grouped launch, 5) SwiGLU + Q8_1
-    if ((e = launch_gemm_mfma_grouped(w_gate, ws.xp, ws.offsets, E, nullptr, ws.gate_up, H, 2 * I, R, s, w_up, I)) !=
-        hipSuccess)
-        return hip_fail(e, "moe_ffn gate_up");
-    if ((e = launch_swiglu_quantize_q8_1(ws.gate_up, ws.midq, nullptr, I, R, s)) != hipSuccess)
-        return hip_fail(e, "moe_ffn swiglu_quantize");
+    // 4) gate|up of every route's expert in one grouped launch whose epilogue applies
+    //    SwiGLU and writes the Q8_1 input of the down projection (no fp32 gate|up)
+    if ((e = launch_gemm_gate_up_swiglu_q8_1(w_gate, w_up, ws.xp, ws.offsets, E, ws.midq, H, I, R, s)) != hipSuccess)
+        return hip_fail(e, "moe_ffn gate_up_swiglu");
     // 6) down projection, 7) weighted combine back to token order
     if ((e = launch_gemm_mfma_grouped(w_down, ws.midq, ws.offsets, E, nullptr, ws.eout, I, H, R, s)) != hipSuccess)
         return hip_fail(e, "moe_ffn down");

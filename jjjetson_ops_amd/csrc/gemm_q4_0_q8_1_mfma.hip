@@ -41,6 +41,7 @@
 
 #include "mfma_q4q8_tile.hpp"
 #include "q4q8_common.hpp"
+#include "q8_1_quant.hpp"
 
 namespace jjo {
 namespace {
@@ -66,11 +67,19 @@ constexpr int kXUnits = kXsBytes / 16;                   // 1152 16-byte units p
 constexpr int kXRuns = kXUnits / 64;                     // 18 wave-sized (1 KB) runs
 
 
-template <bool kGrouped>
+// kSwiglu (grouped, two stacked matrices): the workgroup's 128 rows are rows
+// 64x..64x+63 of the gate matrix (tile rows 0..63) and of the up matrix (tile rows
+// 64..127), x = blockIdx.x; instead of storing them it writes the Q8_1 bytes of
+// silu(gate) * up for those 64 intermediate values of each route to `midq`
+// (superblock-major over the M routes, as the quantizer lays out a [M][n_split]
+// activation).  n_split is the intermediate size I.
+template <bool kGrouped, bool kSwiglu = false>
 __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     const uint8_t *__restrict__ w_all, const uint8_t *__restrict__ xq, float *__restrict__ y, int K,
     int N, int M, const int32_t *__restrict__ expert_offsets, int n_experts,
-    const int32_t *__restrict__ route_dst, const uint8_t *__restrict__ w2, int n_split) {
+    const int32_t *__restrict__ route_dst, const uint8_t *__restrict__ w2, int n_split,
+    uint8_t *__restrict__ midq = nullptr) {
+    static_assert(kGrouped || !kSwiglu, "the fused SwiGLU epilogue is for the grouped gate|up launch");
     extern __shared__ __align__(16) uint8_t smem[];
 
     const int tid = threadIdx.x;
@@ -130,16 +139,24 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     // [n_split, N) from w2 (expert e's block of each); n_split % BN == 0, so a
     // workgroup's rows come from one of them.
     int n_loc0 = n0, n_mat = N;
-    if (w2 != nullptr) {
-        if (n0 < n_split) {
-            n_mat = n_split;
-        } else {
-            w = w2 + (size_t)expert * (N - n_split) * row_bytes;
-            n_loc0 = n0 - n_split;
-            n_mat = N - n_split;
+    const uint8_t *w_src;
+    if constexpr (kSwiglu) {
+        // Tile rows 0..63: gate rows 64x.., tile rows 64..127: up rows 64x..
+        const int ni0 = blockIdx.x * 64;
+        const uint8_t *wm = st_row < 64 ? w : w2 + (size_t)expert * n_split * row_bytes;
+        w_src = wm + (size_t)min(ni0 + (st_row & 63), n_split - 1) * row_bytes + (size_t)st_half * 36;
+    } else {
+        if (w2 != nullptr) {
+            if (n0 < n_split) {
+                n_mat = n_split;
+            } else {
+                w = w2 + (size_t)expert * (N - n_split) * row_bytes;
+                n_loc0 = n0 - n_split;
+                n_mat = N - n_split;
+            }
         }
+        w_src = w + (size_t)min(n_loc0 + st_row, n_mat - 1) * row_bytes + (size_t)st_half * 36;
     }
-    const uint8_t *w_src = w + (size_t)min(n_loc0 + st_row, n_mat - 1) * row_bytes + (size_t)st_half * 36;
     // This thread's 2 raw Q4_0 blocks (36 bytes) of a stage, in two register sets:
     // stage k lands in set k & 1, two compute phases before it is unpacked.
     uint32_t wr0[9], wr1[9];
@@ -506,6 +523,71 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     else
         stage_loop(std::integral_constant<int, 0>{});
 
+    if constexpr (kSwiglu) {
+        // ---- fused SwiGLU + Q8_1: 8*acc of the 128 x 128 tile -> LDS res[token][row]
+        // (rows 0..63 gate, 64..127 up), then silu(gate) * up quantized per 32-group
+        // of intermediate values with the quantizer's exact arithmetic.
+        __syncthreads();  // every wave is done with the staging buffers
+        float *res = reinterpret_cast<float *>(smem);
+        constexpr int kResStride = BN + 4;  // floats per token (padding against bank conflicts)
+        if (pnarrow) {
+            const int t16 = lane & 15, g4 = lane >> 4;
+#pragma unroll
+            for (int rg = 0; rg < 2; ++rg) {
+                float sum[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sum[i] = acc_p[rg][i] + __shfl_xor(acc_p[rg][i], 32);
+                if (g4 < 2) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        res[(4 * g4 + i) * kResStride + wave * 32 + rg * 16 + t16] = 8.0f * sum[i];
+                }
+            }
+        } else if (narrow) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const f32x4 v = {8.0f * acc[0][0][4 * q], 8.0f * acc[0][0][4 * q + 1], 8.0f * acc[0][0][4 * q + 2],
+                                 8.0f * acc[0][0][4 * q + 3]};
+                *reinterpret_cast<f32x4 *>(res + l32 * kResStride + wave * 32 + 8 * q + 4 * hh) = v;
+            }
+        } else {
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const f32x4 v = {8.0f * acc[rt][ct][4 * q], 8.0f * acc[rt][ct][4 * q + 1],
+                                         8.0f * acc[rt][ct][4 * q + 2], 8.0f * acc[rt][ct][4 * q + 3]};
+                        *reinterpret_cast<f32x4 *>(res + (wm * 64 + ct * 32 + l32) * kResStride + wn * 64 + rt * 32 +
+                                                   8 * q + 4 * hh) = v;
+                    }
+        }
+        __syncthreads();
+        // 8 lanes per (token, 32-group); 16 lanes per token (two groups of 64 values).
+        const int ni0 = blockIdx.x * 64;
+        const int n_valid = min(BM, m_end - m0);
+#pragma unroll 1
+        for (int it = 0; it < BM * 16 / kThreads; ++it) {
+            const int idx = it * kThreads + tid;
+            const int tok = idx >> 4, grp = (idx >> 3) & 1, j = idx & 7;
+            const float *rg = res + tok * kResStride + 32 * grp + 4 * j;
+            const f32x4 g = *reinterpret_cast<const f32x4 *>(rg);
+            const f32x4 u = *reinterpret_cast<const f32x4 *>(rg + 64);
+            const float v0 = swiglu(g.x, u.x), v1 = swiglu(g.y, u.y), v2 = swiglu(g.z, u.z), v3 = swiglu(g.w, u.w);
+            uint32_t ds;
+            const uint32_t qv = quantize_group8(v0, v1, v2, v3, &ds);  // all lanes: the butterfly
+            if (tok < n_valid) {
+                const int n = ni0 + 32 * grp + 4 * j;  // intermediate index of the lane's first value
+                uint8_t *blk = midq + ((size_t)(n / kQSuper) * M + (m0 + tok)) * kQ8BlockBytes;
+                const int iqs = n % kQSuper;
+                *reinterpret_cast<uint32_t *>(blk + 16 + iqs) = qv;
+                if (j == 0) *reinterpret_cast<uint32_t *>(blk + 4 * (iqs / 32)) = ds;
+            }
+        }
+        return;
+    }
+
     // ---- store: y[m][n] = 8 * acc ----
     if (kGrouped && pnarrow) {  // block parities meet across lanes l and l ^ 32
         const int t16 = lane & 15, g4 = lane >> 4;
@@ -589,10 +671,11 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     }
 }
 
-template <bool kGrouped>
+template <bool kGrouped, bool kSwiglu = false>
 hipError_t set_smem_attr() {
-    return ensure_dynamic_lds((const void *)gemm_q4_0_q8_1_mfma_kernel<kGrouped>, kSmemBytes);
+    return ensure_dynamic_lds((const void *)gemm_q4_0_q8_1_mfma_kernel<kGrouped, kSwiglu>, kSmemBytes);
 }
+static_assert(BM * (BN + 4) * 4 <= kSmemBytes, "fused SwiGLU result tile fits the staging LDS");
 
 }  // namespace
 
@@ -618,6 +701,20 @@ hipError_t launch_gemm_mfma_grouped(const void *w, const void *xq, const int32_t
     hipLaunchKernelGGL(gemm_q4_0_q8_1_mfma_kernel<true>, grid, dim3(kThreads), kSmemBytes, stream,
                        (const uint8_t *)w, (const uint8_t *)xq, y, K, N, n_routes, expert_offsets,
                        n_experts, route_dst, (const uint8_t *)w2, n_split);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_gate_up_swiglu_q8_1(const void *w_gate, const void *w_up, const void *xq,
+                                           const int32_t *expert_offsets, int n_experts, void *mid_q8_1, int K,
+                                           int I, int n_routes, hipStream_t stream) {
+    hipError_t e = set_smem_attr<true, true>();
+    if (e != hipSuccess) return e;
+    const int max_tiles = (n_routes + BM - 1) / BM + n_experts;
+    const dim3 grid(I / 64, max_tiles);
+    hipLaunchKernelGGL((gemm_q4_0_q8_1_mfma_kernel<true, true>), grid, dim3(kThreads), kSmemBytes, stream,
+                       (const uint8_t *)w_gate, (const uint8_t *)xq, (float *)nullptr, K, 2 * I, n_routes,
+                       expert_offsets, n_experts, (const int32_t *)nullptr, (const uint8_t *)w_up, I,
+                       (uint8_t *)mid_q8_1);
     return hipGetLastError();
 }
 

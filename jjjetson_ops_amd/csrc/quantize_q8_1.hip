@@ -16,30 +16,10 @@
 #include <hip/hip_fp16.h>
 
 #include "q4q8_common.hpp"
+#include "q8_1_quant.hpp"
 
 namespace jjo {
 namespace {
-
-// ds_swizzle bit-mode pattern: and_mask = 0x1f, xor_mask = `x` (within 32 lanes).
-template <int X>
-__device__ __forceinline__ float swz_xor(float v) {
-    constexpr int pattern = 0x1f | (X << 10);
-    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), pattern));
-}
-
-// v0..v3 are the rounded fp32 products x*d_inv (no contraction into what follows).
-__device__ __forceinline__ uint32_t pack_q(float v0, float v1, float v2, float v3) {
-#pragma clang fp contract(off)
-    const int32_t a = (int32_t)roundf(v0);
-    const int32_t b = (int32_t)roundf(v1);
-    const int32_t c = (int32_t)roundf(v2);
-    const int32_t d = (int32_t)roundf(v3);
-    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
-           ((uint32_t)(d & 0xff) << 24);
-}
-
-// silu(g) * u exactly as swiglu_silu_mul_kernel (src/cuda/swiglu.cu:5-14).
-__device__ __forceinline__ float swiglu(float g, float u) { return g * (1.0f / (1.0f + expf(-g))) * u; }
 
 // SWIGLU: the quantized value is silu(gate) * up, with gate = x[m*ldx + i] and
 // up = x[m*ldx + K + i] (the two halves of a [rows][2K] gate|up matrix);
@@ -68,31 +48,15 @@ __global__ __launch_bounds__(256) void quantize_q8_1_kernel(const float *__restr
         if (live) v = *reinterpret_cast<const float4 *>(x + (z * ne1 + m) * K + i0);
     }
 
-    float amax = fmaxf(fabsf(v.x), fmaxf(fabsf(v.y), fmaxf(fabsf(v.z), fabsf(v.w))));
-    float sum = v.x + v.y;
-    sum = sum + v.z;
-    sum = sum + v.w;
-    amax = fmaxf(amax, swz_xor<4>(amax));
-    sum = sum + swz_xor<4>(sum);
-    amax = fmaxf(amax, swz_xor<2>(amax));
-    sum = sum + swz_xor<2>(sum);
-    amax = fmaxf(amax, swz_xor<1>(amax));
-    sum = sum + swz_xor<1>(sum);
-
-    const float d_inv = (amax > 0.0f) ? 127.0f / amax : 0.0f;
-    const uint32_t q = pack_q(v.x * d_inv, v.y * d_inv, v.z * d_inv, v.w * d_inv);
+    uint32_t ds;
+    const uint32_t q = quantize_group8(v.x, v.y, v.z, v.w, &ds);
 
     const int64_t blk = z * slice_blocks + (i0 / kQSuper) * ne1 + m;
     uint8_t *out = y + blk * kQ8BlockBytes;
     const int iqs = (int)(i0 % kQSuper);
     if (live) {
         *reinterpret_cast<uint32_t *>(out + 16 + iqs) = q;
-        if ((iqs & 31) == 0) {
-            const __half hd = __float2half_rn(1.0f / d_inv);
-            const __half hs = __float2half_rn(sum);
-            const uint32_t ds = (uint32_t)__half_as_ushort(hd) | ((uint32_t)__half_as_ushort(hs) << 16);
-            *reinterpret_cast<uint32_t *>(out + 4 * (iqs / 32)) = ds;
-        }
+        if ((iqs & 31) == 0) *reinterpret_cast<uint32_t *>(out + 4 * (iqs / 32)) = ds;
     } else {
         // Groups past K in the last superblock: deterministic zero bytes.
         *reinterpret_cast<uint32_t *>(out + 16 + iqs) = 0u;

@@ -276,6 +276,10 @@ def test_config5_moe_ffn_full_size(dev):
     mq_d = torch.empty(R * I // 128 * 144, dtype=torch.uint8, device=dev)
     mid_d = torch.empty(R * I, dtype=torch.float32, device=dev)
     capi.swiglu_quantize(gu_d, mq_d, R, I, mid_f32=mid_d)
+    # the fused gate|up + SwiGLU + Q8_1 launch the FFN entry runs: the same bytes
+    mq_f = torch.empty_like(mq_d)
+    capi.moe_gate_up_swiglu(d_wg, d_wu, xp_d, off_d, E, mq_f, H, I, R)
+    assert torch.equal(mq_f, mq_d)
     eo_d = torch.empty(R * H, dtype=torch.float32, device=dev)
     capi.grouped_mat_mul(d_wd, mq_d, off_d, eo_d, I, H, R)
     y2 = torch.empty(T * H, dtype=torch.float32, device=dev)

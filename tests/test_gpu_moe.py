@@ -192,6 +192,32 @@ def test_moe_gate_up(T, H, I, E, top_k, dev):
                                    atol=ATOL)
 
 
+@pytest.mark.parametrize("T,H,I,E,top_k", MOE_CASES + [(3, 256, 256, 2, 2), (200, 128, 128, 2, 1)])
+def test_moe_gate_up_swiglu_fused(T, H, I, E, top_k, dev):
+    """The fused gate|up + SwiGLU + Q8_1 launch writes exactly the bytes of the
+    unfused chain (grouped gate|up GEMM into fp32, then the SwiGLU quantizer); the
+    cases cover wide tiles, narrow tails (<= 32 and <= 8 routes of an expert) and
+    experts with no routes."""
+    import torch
+    note(f"moe_gate_up_swiglu T={T} H={H} I={I} E={E} k={top_k}")
+    rng = np.random.default_rng(500 + T)
+    R = T * top_k
+    ids = rng.integers(0, E, size=R).astype(np.int32)
+    off, _, _ = oracle_np.moe_dispatch(ids, E)
+    x = rng.standard_normal((R, H)).astype(np.float32)
+    xp = to_dev(c_oracle.quantize_q8_1(x, [H, R]), dev)
+    wg = to_dev(np.concatenate([make_w(I, H, rng) for _ in range(E)]), dev)
+    wu = to_dev(np.concatenate([make_w(I, H, rng) for _ in range(E)]), dev)
+    off_d = to_dev(off, dev)
+    gu = torch.empty(R * 2 * I, dtype=torch.float32, device=dev)
+    capi.moe_gate_up(wg, wu, xp, off_d, E, gu, H, I, R)
+    mq_ref = torch.empty(R * I // 128 * 144, dtype=torch.uint8, device=dev)
+    capi.swiglu_quantize(gu, mq_ref, R, I)
+    mq = torch.full((R * I // 128 * 144,), 0xA5, dtype=torch.uint8, device=dev)
+    capi.moe_gate_up_swiglu(wg, wu, xp, off_d, E, mq, H, I, R)
+    assert np.array_equal(host(mq), host(mq_ref))
+
+
 @pytest.mark.parametrize("rows,I", [(64, 384), (5, 128), (300, 256)])
 def test_swiglu_quantize(rows, I, dev):
     import torch
