@@ -435,8 +435,8 @@ def main():
     torch.cuda.set_device(dev)
 
     plan = [
-        ("gemv_m1_k4096_n11008", 1, 4096, 11008, 1, args.steps),
         ("gemv_m1_k4096_n11008_split", 1, 4096, 11008, 1, args.steps),
+        ("gemv_m1_k4096_n11008", 1, 4096, 11008, 1, args.steps),
         ("gemv_m1_k11008_n4096_split", 1, 11008, 4096, 1, args.steps),
         ("gemv_m1_k11008_n4096", 1, 11008, 4096, 1, args.steps),
         ("m4_k4096_n14336", 4, 4096, 14336, 2, args.steps),
@@ -478,9 +478,9 @@ def main():
         print(json.dumps(res), flush=True)
         return
 
-    log("bench: headline GEMV M=1 K=4096 N=11008")
+    log("bench: headline GEMV M=1 K=4096 N=11008 (split weight layout)")
     name, M, K, N, seed, st = plan[0]
-    head = time_linear(name, M, K, N, seed, dev, st, args.warmup)
+    head = time_linear(name, M, K, N, seed, dev, st, args.warmup, split=True)
     configs = [head]
     if not args.quick:
         for name, M, K, N, seed, st in plan[1:]:
@@ -504,11 +504,12 @@ def main():
     # The step at M = 1 is a single kernel (fused quantize + GEMV): it is the dominant
     # (only) kernel, and its average duration is the step's.
     roof = {"bound": "hbm", "achieved": head["step_GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": head["step_GBps"] / HBM_PEAK_GBS, "traffic": _traffic("gemv_m1_k4096_n11008"),
-            "kernel": "gemv_q4_0_q8_1_kernel<1,4,1,4,fused,1>", "alg_bytes_per_launch": head["step_alg_bytes"],
+            "frac": head["step_GBps"] / HBM_PEAK_GBS, "traffic": _traffic("gemv_m1_k4096_n11008_split"),
+            "kernel": "gemv_q4s_kernel<1,4,1,4,fused,1>", "weight_layout": "split (nibble plane + fp16 scale plane)",
+            "alg_bytes_per_launch": head["step_alg_bytes"],
             "kernel_us_avg": head["us_per_step"],
             "timing": "back-to-back launches on the launch stream, enqueued behind a device spin, torch.cuda.Event around exactly `steps` launches",
-            "q8_1_input_kernel": {"kernel": "gemv_q4_0_q8_1_kernel<1,2,1,8,q8_1,1>",
+            "q8_1_input_kernel": {"kernel": "gemv_q4s_kernel<1,4,1,4,q8_1,1>",
                                   "us_avg": head["kernel_us_avg"], "GBps": head["kernel_GBps"],
                                   "frac": head["kernel_hbm_frac"]}}
     floor = next((c for c in configs if c["name"].startswith("read_floor")), None)
@@ -518,6 +519,12 @@ def main():
         roof["read_floor"] = {"us": floor["us_per_launch"], "GBps": floor["GBps"], "frac": floor["hbm_frac"],
                               "step_over_floor": head["us_per_step"] / floor["us_per_launch"]}
     gemm = next((c for c in configs if c["name"] == "prefill_m2048_k4096_n14336"), None)
+    gemm_s = next((c for c in configs if c["name"] == "prefill_m2048_k4096_n14336_split"), None)
+    ref_step = next((c for c in configs if c["name"] == "gemv_m1_k4096_n11008"), None)
+    if ref_step is not None:
+        # The same step on the reference's block_q4_0 layout (no repack).
+        roof["block_q4_0_layout_step"] = {"us": ref_step["us_per_step"], "GBps": ref_step["step_GBps"],
+                                          "frac": ref_step["step_GBps"] / HBM_PEAK_GBS}
     line = {
         "metric": METRIC,
         "value": head["step_weight_GBps"],
@@ -531,12 +538,15 @@ def main():
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic (Q4_0 from N(0,0.02), x N(0,1) with 0.1% outlier channels x20; weights rotated over >512 MB)",
-        "config": {"workload": "decode step: quantize x to Q8_1 + Q4_0xQ8_1 GEMV (fused), M=1 K=4096 N=11008",
+        "config": {"workload": "decode step: quantize x to Q8_1 + Q4_0xQ8_1 GEMV (fused), M=1 K=4096 N=11008, "
+                               "weights repacked once into the split layout",
                    "M": 1, "K": 4096, "N": 11008},
         "roofline": roof,
         "cpu_baseline": cpu,
         "gemm_m2048": None if gemm is None else {
-            "TOPS": gemm["kernel_TOPS"], "frac_int8_peak": gemm["kernel_mfma_frac"], "us": gemm["kernel_us_avg"]},
+            "TOPS": gemm["kernel_TOPS"], "frac_int8_peak": gemm["kernel_mfma_frac"], "us": gemm["kernel_us_avg"],
+            "split_layout": None if gemm_s is None else {"TOPS": gemm_s["kernel_TOPS"], "us": gemm_s["kernel_us_avg"],
+                                                         "frac_int8_peak": gemm_s["kernel_mfma_frac"]}},
         "configs": configs,
     }
     print(json.dumps(line), flush=True)

@@ -406,7 +406,18 @@ int q4_0_to_split_device(const void *d_w_q4_0, void *d_w_split, int nrows, int n
 namespace {
 // Split-layout matmul from Q8_1 blocks (shapes validated by the caller).
 int run_mm_split(const void *w, const void *xq, float *y, int K, int N, int M, hipStream_t s) {
-    if (M <= kGemvMaxBatch && K <= kGemvMaxK && (int64_t)M * (K / kQK) * 48 <= 150 * 1024) {
+    const bool gemv_ok = M <= kGemvMaxBatch && K <= kGemvMaxK && (int64_t)M * (K / kQK) * 48 <= 150 * 1024;
+    // The crossovers of the block_q4_0 AUTO dispatch: the GEMV up to batch 4 (one
+    // K slice) or 2, the LDS-resident skinny kernel for 5..16, the GEMM above.
+    if (gemv_ok && M <= (K <= 4096 ? kGemvPreferredBatch : 2)) {
+        hipError_t e = launch_gemv_q4s(w, xq, y, K, N, M, s);
+        return e == hipSuccess ? JJO_OK : hip_fail(e, "gemv_q4s launch");
+    }
+    if (M <= 16 && gemm_skinny_persist_supported(w, xq, K, M)) {
+        hipError_t e = launch_gemm_skinny_persist_layout(w, xq, y, K, N, M, true, s);
+        return e == hipSuccess ? JJO_OK : hip_fail(e, "gemm_skinny_persist (split layout) launch");
+    }
+    if (gemv_ok) {
         hipError_t e = launch_gemv_q4s(w, xq, y, K, N, M, s);
         return e == hipSuccess ? JJO_OK : hip_fail(e, "gemv_q4s launch");
     }

@@ -331,9 +331,10 @@ hipError_t launch_gemm_q4s_mfma(const void *w, const void *xq, float *y, int K, 
     // Two workgroups per CU: when the tiles leave a partial last round of at most
     // half the slots, that round's tiles run as 64-token halves (twice the
     // workgroups, each half the work), so every slot of the last round is busy.
+    // A batch whose tiles do not fill the slots runs every tile as two halves.
     const int64_t slots = 2 * (int64_t)device_cu_count();
     const int64_t rem = slots > 0 ? tiles % slots : 0;
-    const int64_t n_split = (tiles > slots && rem > 0 && 2 * rem <= slots) ? rem : 0;
+    const int64_t n_split = tiles < slots ? tiles : (rem > 0 && 2 * rem <= slots) ? rem : 0;
     const int64_t n_full = tiles - n_split;
     const int64_t grid = n_full + 2 * n_split;
     if (grid > 0x7fffffffLL) return hipErrorInvalidValue;

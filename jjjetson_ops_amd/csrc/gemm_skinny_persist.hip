@@ -33,6 +33,11 @@
 //   * The 8 waves' K-slice partials of each tile are added through LDS in wave
 //     order at the end (deterministic).
 //
+// SPLIT: weights in the split layout (nibble plane + fp16 scale plane).  An item
+// is then the 16 rows' 8 nibble blocks (16 x 128 bytes, gathered by two DMA
+// instructions) followed by their 16 x 8 scales (one DMA instruction of 16 lanes):
+// the same 2304 bytes and three DMA instructions, and every operand read aligned.
+//
 // Requirements (checked by the launcher): M <= 16, K % 256 == 0, w and xq 16-byte aligned.
 #include <hip/hip_fp16.h>
 
@@ -80,7 +85,7 @@ __device__ __forceinline__ void dma16(const void *src, uint32_t lds_base) {
                  : "memory");
 }
 
-template <bool PAIR>
+template <bool PAIR, bool SPLIT>
 __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uint8_t *__restrict__ w,
                                                                         const uint8_t *__restrict__ xq,
                                                                         float *__restrict__ y, int K, int N, int M,
@@ -123,6 +128,23 @@ __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uin
         auto issue = [&](int it, int j, int t) {  // item it = (stage wave + 8j, tile t)
             const int s = wave + kPW * j;
             uint8_t *slot = ring + (it % kPRing) * kPItemBytes;
+            if constexpr (SPLIT) {
+                // Nibbles: chunk c = 64*i + lane -> row c / 8, block c % 8 of the stage;
+                // then the 16 rows' 8 scales (16 bytes per row, 16-byte aligned since
+                // nb % 8 == 0).  Rows past N re-read row N-1 (never stored).
+                const int blk0 = (k0 / kQK) + s * kPStageBlocks;
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int c = 64 * i + lane;
+                    const int r = min((tile0 + t) * 16 + (c >> 3), N - 1);
+                    dma16(w + ((size_t)r * nb + blk0 + (c & 7)) * 16, (uint32_t)(uintptr_t)(slot + 1024 * i));
+                }
+                if (lane < 16) {
+                    const int r = min((tile0 + t) * 16 + lane, N - 1);
+                    dma16(w + (size_t)N * nb * 16 + ((size_t)r * nb + blk0) * 2,
+                          (uint32_t)(uintptr_t)(slot + 2048));
+                }
+            } else {
             const uint8_t *base = w + (size_t)((k0 / kQK) + s * kPStageBlocks) * kQ4BlockBytes;
             // Three DMA instructions per item (the third with lanes 0..15 only): chunk
             // c = 64*i + lane -> row c / 9, 16-byte piece c % 9 of the row's 144 bytes,
@@ -133,6 +155,7 @@ __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uin
                 const int r = min((tile0 + t) * 16 + c / 9, N - 1);
                 const uint8_t *src = base + (size_t)r * row_bytes + 16u * (uint32_t)(c % 9);
                 if (i < 2 || lane < kPItemChunks - 128) dma16(src, (uint32_t)(uintptr_t)(slot + 1024 * i));
+            }
             }
         };
 
@@ -220,26 +243,41 @@ __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uin
                 if (it + 1 < n_items) JJO_P_VMCNT(3); else JJO_P_VMCNT(0);  // item it has landed
                 const uint8_t *slot = ring + (it % kPRing) * kPItemBytes;
                 const uint8_t *wr0 = slot + l16 * kPRowBytes;
+                const uint8_t *wq_s = slot + l16 * 128;                 // split: row's 8 nibble blocks
+                const _Float16 *wd_s = reinterpret_cast<const _Float16 *>(slot + 2048 + l16 * 16);  // its 8 scales
                 {
-                    const _Float16 *dr = reinterpret_cast<const _Float16 *>(wr0 + (g & 1) * 4 * kQ4BlockBytes);
                     f16x4 dw_op;
+                    if constexpr (SPLIT) {
+                        dw_op = *reinterpret_cast<const f16x4 *>(wd_s + 4 * (g & 1));
+                    } else {
+                        const _Float16 *dr = reinterpret_cast<const _Float16 *>(wr0 + (g & 1) * 4 * kQ4BlockBytes);
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) dw_op[q] = dr[q * kQ4BlockBytes / 2];
+                        for (int q = 0; q < 4; ++q) dw_op[q] = dr[q * kQ4BlockBytes / 2];
+                    }
                     acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(sx_op, dw_op, acc[t], 0, 0, 0);
                 }
 #pragma unroll
                 for (int p = 0; p < kPStageBlocks / 2; ++p) {
-                    // qs bytes 8kc..8kc+7 of block 2p + po of this lane's weight row: at byte
-                    // 18*bb + 2 + 8kc of the row, 2 mod 4 for even blocks, 0 mod 4 for odd ones.
-                    const int off = (2 * p + po) * kQ4BlockBytes + 2 + 8 * kc;
-                    const uint32_t *pp = reinterpret_cast<const uint32_t *>(wr0 + (off & ~3));
-                    const uint32_t sh = off & 3;
-                    const uint32_t d0 = pp[0], d1 = pp[1], d2 = pp[sh ? 2 : 1];
-                    const uint32_t q0 = __builtin_amdgcn_alignbyte(d1, d0, sh);
-                    const uint32_t q1 = __builtin_amdgcn_alignbyte(d2, d1, sh);
+                    uint32_t q0, q1;
+                    _Float16 dw;
+                    if constexpr (SPLIT) {
+                        const uint2 qq = *reinterpret_cast<const uint2 *>(wq_s + (2 * p + po) * 16 + 8 * kc);
+                        q0 = qq.x;
+                        q1 = qq.y;
+                        dw = wd_s[2 * p + po];
+                    } else {
+                        // qs bytes 8kc..8kc+7 of block 2p + po of this lane's weight row: at byte
+                        // 18*bb + 2 + 8kc of the row, 2 mod 4 for even blocks, 0 mod 4 for odd ones.
+                        const int off = (2 * p + po) * kQ4BlockBytes + 2 + 8 * kc;
+                        const uint32_t *pp = reinterpret_cast<const uint32_t *>(wr0 + (off & ~3));
+                        const uint32_t sh = off & 3;
+                        const uint32_t d0 = pp[0], d1 = pp[1], d2 = pp[sh ? 2 : 1];
+                        q0 = __builtin_amdgcn_alignbyte(d1, d0, sh);
+                        q1 = __builtin_amdgcn_alignbyte(d2, d1, sh);
+                        dw = *reinterpret_cast<const _Float16 *>(wr0 + (2 * p + po) * kQ4BlockBytes);
+                    }
                     const i32x4 bop = i32x4{(int32_t)(q0 & 0x0f0f0f0fu), (int32_t)(q1 & 0x0f0f0f0fu),
                                             (int32_t)((q0 >> 4) & 0x0f0f0f0fu), (int32_t)((q1 >> 4) & 0x0f0f0f0fu)};
-                    const _Float16 dw = *reinterpret_cast<const _Float16 *>(wr0 + (2 * p + po) * kQ4BlockBytes);
                     const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop[p], bop, bias, 0, 0, 0);
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
@@ -299,25 +337,37 @@ __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uin
                 if (it + 1 < n_items) JJO_P_VMCNT(3); else JJO_P_VMCNT(0);  // item it has landed
                 const uint8_t *slot = ring + (it % kPRing) * kPItemBytes;
                 const uint8_t *wr0 = slot + l16 * kPRowBytes;
+                const uint8_t *wq_s = slot + l16 * 128;
+                const _Float16 *wd_s = reinterpret_cast<const _Float16 *>(slot + 2048 + l16 * 16);
                 // s_x term: d_w of blocks 4(g&1)..4(g&1)+3 of this lane's weight row
                 {
-                    const _Float16 *dr = reinterpret_cast<const _Float16 *>(wr0 + (g & 1) * 4 * kQ4BlockBytes);
                     f16x4 dw_op;
+                    if constexpr (SPLIT) {
+                        dw_op = *reinterpret_cast<const f16x4 *>(wd_s + 4 * (g & 1));
+                    } else {
+                        const _Float16 *dr = reinterpret_cast<const _Float16 *>(wr0 + (g & 1) * 4 * kQ4BlockBytes);
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) dw_op[q] = dr[q * kQ4BlockBytes / 2];
+                        for (int q = 0; q < 4; ++q) dw_op[q] = dr[q * kQ4BlockBytes / 2];
+                    }
                     acc[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(sx_op, dw_op, acc[t], 0, 0, 0);
                 }
 #pragma unroll
                 for (int bb = 0; bb < kPStageBlocks; ++bb) {
-                    const uint8_t *wr = wr0 + bb * kQ4BlockBytes;
                     uint32_t q;
-                    if ((bb & 1) == 0) {  // nibble dword g at 2 mod 4: re-align
-                        const uint32_t *p = reinterpret_cast<const uint32_t *>(wr + 4 * g);
-                        q = __builtin_amdgcn_alignbyte(p[1], p[0], 2);
+                    _Float16 dw;
+                    if constexpr (SPLIT) {
+                        q = *reinterpret_cast<const uint32_t *>(wq_s + bb * 16 + 4 * g);
+                        dw = wd_s[bb];
                     } else {
-                        q = *reinterpret_cast<const uint32_t *>(wr + 2 + 4 * g);
+                        const uint8_t *wr = wr0 + bb * kQ4BlockBytes;
+                        if ((bb & 1) == 0) {  // nibble dword g at 2 mod 4: re-align
+                            const uint32_t *p = reinterpret_cast<const uint32_t *>(wr + 4 * g);
+                            q = __builtin_amdgcn_alignbyte(p[1], p[0], 2);
+                        } else {
+                            q = *reinterpret_cast<const uint32_t *>(wr + 2 + 4 * g);
+                        }
+                        dw = *reinterpret_cast<const _Float16 *>(wr);
                     }
-                    const _Float16 dw = *reinterpret_cast<const _Float16 *>(wr);
                     const long bop = (long)((uint64_t)((q >> 4) & 0x0f0f0f0fu) << 32 | (q & 0x0f0f0f0fu));
                     const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop[bb], bop, bias, 0, 0, 0);
 #pragma unroll
@@ -370,23 +420,33 @@ bool gemm_skinny_persist_supported(const void *w, const void *xq, int K, int M) 
     return K % 256 == 0 && M >= 1 && M <= 16 && ((uintptr_t)w & 15) == 0 && ((uintptr_t)xq & 15) == 0;
 }
 
-hipError_t launch_gemm_skinny_persist(const void *w, const void *xq, float *y, int K, int N, int M,
-                                      hipStream_t stream) {
+hipError_t launch_gemm_skinny_persist_layout(const void *w, const void *xq, float *y, int K, int N, int M, bool split,
+                                             hipStream_t stream) {
     if (!gemm_skinny_persist_supported(w, xq, K, M)) return hipErrorInvalidValue;
-    const void *kern = M <= 8 ? (const void *)gemm_skinny_persist_kernel<true>
-                              : (const void *)gemm_skinny_persist_kernel<false>;
+    const void *kern = M <= 8 ? (split ? (const void *)gemm_skinny_persist_kernel<true, true>
+                                       : (const void *)gemm_skinny_persist_kernel<true, false>)
+                              : (split ? (const void *)gemm_skinny_persist_kernel<false, true>
+                                       : (const void *)gemm_skinny_persist_kernel<false, false>);
     hipError_t e = ensure_dynamic_lds(kern, kPSmemBytes);
     if (e != hipSuccess) return e;
     const int n_tiles = (N + 15) / 16;
     const int tiles_per_wg = min(kPMaxTiles, (n_tiles + 255) / 256);
     const int blocks = (n_tiles + tiles_per_wg - 1) / tiles_per_wg;
-    if (M <= 8)
-        hipLaunchKernelGGL(gemm_skinny_persist_kernel<true>, dim3(blocks), dim3(64 * kPW), kPSmemBytes, stream,
-                           (const uint8_t *)w, (const uint8_t *)xq, y, K, N, M, tiles_per_wg);
-    else
-        hipLaunchKernelGGL(gemm_skinny_persist_kernel<false>, dim3(blocks), dim3(64 * kPW), kPSmemBytes, stream,
-                           (const uint8_t *)w, (const uint8_t *)xq, y, K, N, M, tiles_per_wg);
+#define JJO_P_LAUNCH(P, S)                                                                                    \
+    hipLaunchKernelGGL((gemm_skinny_persist_kernel<P, S>), dim3(blocks), dim3(64 * kPW), kPSmemBytes, stream, \
+                       (const uint8_t *)w, (const uint8_t *)xq, y, K, N, M, tiles_per_wg)
+    if (M <= 8) {
+        if (split) JJO_P_LAUNCH(true, true); else JJO_P_LAUNCH(true, false);
+    } else {
+        if (split) JJO_P_LAUNCH(false, true); else JJO_P_LAUNCH(false, false);
+    }
+#undef JJO_P_LAUNCH
     return hipGetLastError();
+}
+
+hipError_t launch_gemm_skinny_persist(const void *w, const void *xq, float *y, int K, int N, int M,
+                                      hipStream_t stream) {
+    return launch_gemm_skinny_persist_layout(w, xq, y, K, N, M, false, stream);
 }
 
 }  // namespace jjo

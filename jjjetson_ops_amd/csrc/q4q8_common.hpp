@@ -65,6 +65,9 @@ hipError_t launch_gemm_skinny(const void *w, const void *xq, float *y, int K, in
 bool gemm_skinny_persist_supported(const void *w, const void *xq, int K, int M);
 hipError_t launch_gemm_skinny_persist(const void *w, const void *xq, float *y, int K, int N, int M,
                                       hipStream_t stream);
+// The same kernel with the weights in either layout (split: nibble + scale planes).
+hipError_t launch_gemm_skinny_persist_layout(const void *w, const void *xq, float *y, int K, int N, int M, bool split,
+                                             hipStream_t stream);
 // tile_rows: 64, or 32 (the stage's blocks split between wave pairs).
 hipError_t launch_gemm_mfma64(const void *w, const void *xq, float *y, int K, int N, int M,
                               hipStream_t stream, int tile_rows);

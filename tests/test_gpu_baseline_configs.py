@@ -5,7 +5,8 @@
             the dequantized fp32 product that the oracle itself does not enter
   config 2  M=1 decode, K=4096->N=11008 and K=11008->N=4096, weights seed 1,
             quantized on device each call (the fused entry): every output checked
-  config 3  M in {4, 8, 16}, K=4096, N=14336, weights seed 2, through AUTO
+  config 3  M in {4, 8, 16}, K=4096, N=14336, weights seed 2, through AUTO, and through
+            the split weight layout (repacked on the device)
   config 5  8 experts, top-2 of N(0,1) router logits [512, 8] (seed 4), 512 tokens,
             K=4096 -> N=14336 in ONE grouped launch, outputs scattered per route;
             and the whole Q4_0 MoE FFN of that layer (I=14336) stage by stage
@@ -160,6 +161,15 @@ def test_config3_small_batch(M, dev):
     rows = np.unique(np.concatenate([rng.choice(N, 1500, replace=False), [0, 15, 16, 31, 32, N - 1]]))
     exp = c_oracle.matmul(sub_weights(w, rows, K), xq, K, rows.size, M)
     np.testing.assert_allclose(got[:, rows], exp, rtol=RTOL, atol=ATOL)
+    # the same weights repacked into the split layout on the device, through the
+    # split entry with the fp32 activation (quantize + matmul)
+    ws = torch.empty_like(w_d)
+    capi.q4_0_to_split(w_d, ws, N, K)
+    xq2 = torch.zeros_like(xq_d)
+    y2 = torch.full((M * N,), float("nan"), dtype=torch.float32, device=dev)
+    capi.mat_mul_split_f32(ws, to_dev(x, dev), xq2, y2, K, N, M)
+    assert np.array_equal(host(xq2), xq)
+    np.testing.assert_allclose(host(y2).reshape(M, N)[:, rows], exp, rtol=RTOL, atol=ATOL)
 
 
 # ------------------------------------------------------------------ config 5

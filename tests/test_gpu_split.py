@@ -127,7 +127,8 @@ def test_split_f32_batch(M, dev):
 
 
 @pytest.mark.parametrize("K,N,M", [(4096, 256, 128), (4096, 300, 130), (384, 64, 257), (128, 96, 9),
-                                   (11008, 128, 64), (512, 4100, 96)])
+                                   (11008, 128, 64), (512, 4100, 96), (4096, 257, 5), (4096, 1000, 8),
+                                   (11264, 77, 12), (256, 33, 16), (4096, 14336, 16), (4096, 70, 17)])
 def test_split_gemm(K, N, M, dev):
     import torch
     note(f"split gemm M={M} K={K} N={N}")
