@@ -279,12 +279,10 @@ __global__ __launch_bounds__(g2::kThreads, 2) void gemm_q4s_mfma_kernel(const ui
                 store_w(buf ^ 1);
                 __syncthreads();    // publishes stage c+1, retires the reads of buffer `buf`
                 zero_tail_headers(buf ^ 1);
-    #if !defined(JJO_EXP_NOLOAD)
                 if (c + 2 < n_stages) {
                     dma_x(c + 2, buf);
                     load_w(c + 2, buf);
                 }
-    #endif
             }
         }
 

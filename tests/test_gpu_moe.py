@@ -192,12 +192,13 @@ def test_moe_gate_up(T, H, I, E, top_k, dev):
                                    atol=ATOL)
 
 
-@pytest.mark.parametrize("T,H,I,E,top_k", MOE_CASES + [(3, 256, 256, 2, 2), (200, 128, 128, 2, 1)])
+@pytest.mark.parametrize("T,H,I,E,top_k", MOE_CASES + [(3, 256, 256, 2, 2), (200, 128, 128, 2, 1),
+                                                     (160, 256, 128, 1, 1), (330, 128, 256, 2, 1)])
 def test_moe_gate_up_swiglu_fused(T, H, I, E, top_k, dev):
     """The fused gate|up + SwiGLU + Q8_1 launch writes exactly the bytes of the
     unfused chain (grouped gate|up GEMM into fp32, then the SwiGLU quantizer); the
-    cases cover wide tiles, narrow tails (<= 32 and <= 8 routes of an expert) and
-    experts with no routes."""
+    cases cover experts of <= 8, <= 32, 160 (five column tiles in one chunk) and
+    about 165 routes (two chunks), and experts with no routes."""
     import torch
     note(f"moe_gate_up_swiglu T={T} H={H} I={I} E={E} k={top_k}")
     rng = np.random.default_rng(500 + T)

@@ -387,11 +387,11 @@ def test_grouped_moe_small(dev):
 
 
 @pytest.mark.parametrize("counts", [[1, 129, 0, 31, 160, 32, 33, 7], [3, 2, 1, 4], [64, 65, 0, 96, 1, 200],
-                                    [8, 9, 136, 137, 5, 6]])
+                                    [8, 9, 136, 137, 5, 6], [161, 320, 321, 481, 0, 2]])
 def test_grouped_tail_tiles(counts, dev):
-    """Expert tails of 1..33 routes (at most 8 valid tokens run the paired-block
-    narrow layout, 9..32 the 32-wide narrow layout), empty experts, and a full tile
-    followed by a tail; every output row is checked against the oracle."""
+    """Experts of 1..33 routes (one narrow chunk of 1..2 column tiles), 129..160 (one
+    chunk of up to 5 column tiles), 161..481 (2..4 equal chunks, the last ones
+    ragged), and empty experts; every output row is checked against the oracle."""
     import torch
     E, K, N = len(counts), 512, 256
     note(f"grouped tails counts={counts}")
