@@ -678,7 +678,11 @@ constexpr int rg_for() {
 template <int M, int JS, bool FUSED = false>
 constexpr int rg_for_s() {
     if (M == 1 && FUSED && JS == 1) return JJO_Q4S_RG1F;
-    if (M == 1) return JS == 1 ? JJO_Q4S_RG1 : JS == 2 ? 4 : JS == 3 ? 4 : 2;
+    // Three K slices (K 8193..12288): the Q8_1-input kernel prefers twice the
+    // workgroups of half the rows (K=11008, N=4096: 6.25-6.59 against 6.65-6.88 us,
+    // with two rows per wave); the fused step keeps four row groups, since every
+    // workgroup re-stages the fp32 x (44 KB at K=11008).
+    if (M == 1) return JS == 1 ? JJO_Q4S_RG1 : JS == 2 ? 4 : JS == 3 ? (FUSED ? 4 : 2) : 2;
     return JS == 1 ? kRgM : JS == 2 ? 2 : 1;
 }
 
@@ -721,7 +725,7 @@ hipError_t launch_m(const void *w, const void *xin, uint8_t *xq_out, float *y, i
     switch (js) {
         case 1: return launch_js<SPLIT, M, U, 1, FUSED>(w, xin, xq_out, y, K, N, stream);
         case 2: return launch_js<SPLIT, M, U, 2, FUSED>(w, xin, xq_out, y, K, N, stream);
-        case 3: return launch_js<SPLIT, M, U, 3, FUSED>(w, xin, xq_out, y, K, N, stream);
+        case 3: return launch_js<SPLIT, M, (SPLIT && M == 1 && !FUSED) ? 2 : U, 3, FUSED>(w, xin, xq_out, y, K, N, stream);
         case 4: return launch_js<SPLIT, M, U, 4, FUSED>(w, xin, xq_out, y, K, N, stream);
         default: return hipErrorInvalidValue;  // K > 16384: the C ABI routes these to the MFMA GEMM
     }

@@ -61,7 +61,7 @@ def _weights(rng, N, K):
 
 
 @pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
-@pytest.mark.parametrize("K,N", [(128, 77), (4096, 1000), (11008, 300), (16384, 64)])
+@pytest.mark.parametrize("K,N", [(128, 77), (4096, 1000), (11008, 300), (11008, 77), (16384, 64)])
 def test_split_matmul_q8_1_input(M, K, N, dev):
     import torch
     if M * (K // 32) * 48 > 150 * 1024:
