@@ -233,6 +233,17 @@ int linear_q4_0_forward_device(void *stream, void *quant_workspace, const float 
                                int out_features, int num_tokens);
 
 /*
+ * linear_q4_0_forward_device on weights repacked once into the split layout
+ * (q4_0_to_split / q4_0_to_split_device; 16-byte aligned): the engine's fast path
+ * when it repacks at load time, beside the same linear_forward_device slot.  Same
+ * arguments, workspace and rules; results follow mat_mul_q4_0s_q8_1_f32_device
+ * (oracle tolerance, not bit-identical to the block_q4_0 entry: other kernels).
+ */
+int linear_q4_0s_forward_device(void *stream, void *quant_workspace, const float *input,
+                                const void *weight_split, float *output, int in_features,
+                                int out_features, int num_tokens);
+
+/*
  * Allocation-free variant of linear_q4_0_forward_device.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The Q8_1

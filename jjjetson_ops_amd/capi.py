@@ -49,6 +49,7 @@ EXPORTED_SYMBOLS = (
     "jjo_read_floor_device",
     "linear_q4_0_workspace_bytes",
     "linear_q4_0_forward_device",
+    "linear_q4_0s_forward_device",
     "linear_q4_0_forward_host",
     "linear_q4_0_noalloc_max_bytes",
     "linear_q4_0_forward_device_noalloc",
@@ -142,6 +143,8 @@ def lib() -> ctypes.CDLL:
         L.linear_q4_0_workspace_bytes.argtypes = [i32, i32]
         L.linear_q4_0_forward_device.restype = i32
         L.linear_q4_0_forward_device.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32]
+        L.linear_q4_0s_forward_device.restype = i32
+        L.linear_q4_0s_forward_device.argtypes = [vp, vp, vp, vp, vp, i32, i32, i32]
         L.linear_q4_0_noalloc_max_bytes.restype = i64
         L.linear_q4_0_noalloc_max_bytes.argtypes = []
         L.linear_q4_0_forward_device_noalloc.restype = i32
@@ -392,6 +395,15 @@ def linear_q4_0(x, w, y, in_features: int, out_features: int, num_tokens: int, w
     _check(lib().linear_q4_0_forward_device(_stream(stream), None if ws is None else _dev(ws, "ws"), _dev(x, "x"),
                                             _dev(w, "w"), _dev(y, "y"), in_features, out_features, num_tokens),
            "linear_q4_0_forward_device")
+
+
+def linear_q4_0_split(x, ws_split, y, in_features: int, out_features: int, num_tokens: int, ws=None,
+                      stream=None) -> None:
+    """linear_q4_0s_forward_device: linear_q4_0 on weights repacked into the split layout."""
+    _check(lib().linear_q4_0s_forward_device(_stream(stream), None if ws is None else _dev(ws, "ws"), _dev(x, "x"),
+                                             _dev(ws_split, "w"), _dev(y, "y"), in_features, out_features,
+                                             num_tokens),
+           "linear_q4_0s_forward_device")
 
 
 def linear_q4_0_noalloc(x, w, y, in_features: int, out_features: int, num_tokens: int, stream=None) -> None:

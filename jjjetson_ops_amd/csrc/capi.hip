@@ -595,6 +595,18 @@ int linear_q4_0_forward_device(void *stream, void *quant_workspace, const float 
                                         num_tokens, stream);
 }
 
+int linear_q4_0s_forward_device(void *stream, void *quant_workspace, const float *input, const void *weight_split,
+                                float *output, int in_features, int out_features, int num_tokens) {
+    clear_error();
+    if (in_features <= 0 || out_features <= 0 || num_tokens <= 0)
+        return set_error(JJO_ERR_INVALID_ARG, "linear_q4_0s: invalid in_features=%d out_features=%d num_tokens=%d",
+                         in_features, out_features, num_tokens);
+    if (input == nullptr || weight_split == nullptr || output == nullptr)
+        return set_error(JJO_ERR_INVALID_ARG, "linear_q4_0s: null pointer argument");
+    return mat_mul_q4_0s_q8_1_f32_device(weight_split, input, quant_workspace, output, in_features, out_features,
+                                         num_tokens, stream);
+}
+
 }  // extern "C"
 
 // ---------------------------------------------------------------- allocation-free engine linear

@@ -71,6 +71,35 @@ def test_linear_q4_0(K, N, T, dev):
     np.testing.assert_allclose(host(y).reshape(T, N), c_oracle.matmul(w, xq, K, N, T), rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("K,N,T", [(4096, 1024, 1), (4096, 300, 7), (1024, 256, 16), (1024, 256, 64),
+                                   (11008, 128, 1)])
+def test_linear_q4_0_split_layout(K, N, T, dev):
+    """The engine linear on weights repacked into the split layout: the oracle's
+    result at the usual bars, the Q8_1 workspace bytes exact when one is used, and
+    bit for bit the split-layout matmul entry it forwards to."""
+    import torch
+    note(f"linear_q4_0s K={K} N={N} T={T}")
+    rng = np.random.default_rng(3 * K + N + T)
+    w = make_w(N, K, rng)
+    x = rng.standard_normal((T, K)).astype(np.float32)
+    wd = to_dev(w, dev)
+    wsplit = torch.empty_like(wd)
+    capi.q4_0_to_split(wd, wsplit, N, K)
+    nq = max(1, capi.linear_q4_0_workspace_bytes(K, T))
+    ws = torch.empty(nq, dtype=torch.uint8, device=dev)
+    y = torch.full((T * N,), float("nan"), dtype=torch.float32, device=dev)
+    xd = to_dev(x, dev)
+    capi.linear_q4_0_split(xd, wsplit, y, K, N, T, ws=ws)
+    xq = c_oracle.quantize_q8_1(x, [K, T])
+    np.testing.assert_allclose(host(y).reshape(T, N), c_oracle.matmul(w, xq, K, N, T), rtol=RTOL, atol=ATOL)
+    if T > 1:
+        assert np.array_equal(host(ws)[:xq.size], xq)
+    y2 = torch.full_like(y, float("nan"))
+    ws2 = torch.empty_like(ws)
+    capi.mat_mul_split_f32(wsplit, xd, ws2, y2, K, N, T)
+    assert np.array_equal(host(y), host(y2))
+
+
 def test_linear_q4_0_host_entry():
     import ctypes
     K, N, T = 512, 96, 3
