@@ -218,7 +218,7 @@ def time_moe(dev, steps, warmup):
             "kernel_hbm_frac": alg_bytes / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
-def time_moe_ffn(dev, steps, warmup):
+def time_moe_ffn(dev, steps, warmup, split=False):
     """The whole Q4_0 MoE FFN of the same layer shape (8 experts, top-2, 512 tokens,
     H=4096, I=14336): quantize, top-k, dispatch, gate|up, SwiGLU+quantize, down,
     combine -- seven launches per step (gate|up, SwiGLU and its Q8_1 quantization are one)."""
@@ -231,12 +231,19 @@ def time_moe_ffn(dev, steps, warmup):
     wg = torch.cat([make_weights(I, H, 60 + e, dev, 1)[0] for e in range(E)])
     wu = torch.cat([make_weights(I, H, 70 + e, dev, 1)[0] for e in range(E)])
     wd = torch.cat([make_weights(H, I, 80 + e, dev, 1)[0] for e in range(E)])
+    if split:  # the load-time repack of each stacked expert matrix
+        def repack(src, rows, k):
+            out = torch.empty_like(src)
+            capi.q4_0_to_split(src, out, rows, k)
+            return out
+        wg, wu, wd = repack(wg, E * I, H), repack(wu, E * I, H), repack(wd, E * H, I)
+        torch.cuda.synchronize()
     x = make_x(T, H, 46, dev, True)
     y = torch.empty(T * H, dtype=torch.float32, device=dev)
     ws = torch.empty(capi.moe_ffn_workspace_bytes(T, H, I, E, topk), dtype=torch.uint8, device=dev)
 
     def step(i):
-        capi.moe_ffn(x, logits, wg, wu, wd, y, T, H, I, E, topk, ws)
+        capi.moe_ffn(x, logits, wg, wu, wd, y, T, H, I, E, topk, ws, split=split)
 
     for i in range(warmup):
         step(i)
@@ -245,7 +252,8 @@ def time_moe_ffn(dev, steps, warmup):
     ops = 2.0 * R * 3 * I * H
     wbytes = 3 * E * I * (H // 32) * 18  # 792 MB: every step streams past the MALL
     torch.cuda.empty_cache()
-    return {"name": "moe_ffn_q4_0_e8_top2_t512_h4096_i14336", "routes": R, "H": H, "I": I,
+    return {"name": "moe_ffn_q4_0_e8_top2_t512_h4096_i14336" + ("_split" if split else ""), "routes": R,
+            "H": H, "I": I, "weight_layout": "split" if split else "block_q4_0",
             "us_per_step": avg * 1e3, "TOPS": ops / (avg * 1e-3) / 1e12,
             "mfma_frac": ops / (avg * 1e-3) / 1e12 / INT8_PEAK_TOPS,
             "weight_GBps": wbytes / (avg * 1e-3) / 1e9, "launches_per_step": 7}

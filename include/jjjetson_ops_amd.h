@@ -215,6 +215,18 @@ int mat_mul_q4_0_q8_1_grouped_device(const void *d_w_q4_0, const void *d_x_q8_1,
                                      int nrows_out, int n_routes, void *stream);
 
 /*
+ * mat_mul_q4_0_q8_1_grouped_device on expert weights repacked into the split layout
+ * (the stacked [E * nrows_out] rows repacked as one matrix, 16-byte aligned).  Same
+ * arguments and rules; the results equal the block_q4_0 entry's bit for bit (the
+ * same kernel, another weight load).  No counterpart beyond the reference's
+ * "offline repacker to the GPU-friendly split layout" (weight_loader.h:12-14).
+ */
+int mat_mul_q4_0s_q8_1_grouped_device(const void *d_w_split, const void *d_x_q8_1,
+                                      const int32_t *d_expert_offsets, int n_experts,
+                                      const int32_t *d_route_dst, float *d_y, int ncols_k,
+                                      int nrows_out, int n_routes, void *stream);
+
+/*
  * Engine linear layer with Q4_0 weights: the slot beside linear_forward_device
  * (src/cuda/linear.h:7-9, called from src/engine/transformer_runner.cpp:214-216,294,
  * 319-327).  Same argument order as the reference with the cuBLAS handle slot
@@ -353,6 +365,13 @@ int moe_q4_0_ffn_forward_device(void *stream, const float *x, const float *logit
                                 const void *w_up, const void *w_down, float *y, int num_tokens, int hidden_size,
                                 int intermediate_size, int num_experts, int top_k, void *workspace,
                                 int64_t workspace_bytes);
+/* The same FFN on expert weights repacked into the split layout (each of gate, up
+ * and down as one [E * rows] matrix, 16-byte aligned); y equals the block_q4_0
+ * entry's bit for bit. */
+int moe_q4_0s_ffn_forward_device(void *stream, const float *x, const float *logits, const void *w_gate_split,
+                                 const void *w_up_split, const void *w_down_split, float *y, int num_tokens,
+                                 int hidden_size, int intermediate_size, int num_experts, int top_k, void *workspace,
+                                 int64_t workspace_bytes);
 
 /* ------------------------------------------------------------------ Q4_0 weights on disk
  * The reference's loader holds F32 tensors only (WeightDtype, src/model/weight_loader.h:12-14;

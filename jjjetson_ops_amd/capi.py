@@ -46,6 +46,7 @@ EXPORTED_SYMBOLS = (
     "mat_mul_q4_0_q8_1_device_algo",
     "mat_mul_q4_0_q8_1_block_sums_device",
     "mat_mul_q4_0_q8_1_grouped_device",
+    "mat_mul_q4_0s_q8_1_grouped_device",
     "jjo_read_floor_device",
     "linear_q4_0_workspace_bytes",
     "linear_q4_0_forward_device",
@@ -61,6 +62,7 @@ EXPORTED_SYMBOLS = (
     "moe_combine_device",
     "moe_q4_0_ffn_workspace_bytes",
     "moe_q4_0_ffn_forward_device",
+    "moe_q4_0s_ffn_forward_device",
     "q4_0_bytes",
     "quantize_q4_0_host",
     "quantize_q4_0_device",
@@ -137,6 +139,8 @@ def lib() -> ctypes.CDLL:
         L.mat_mul_q4_0_q8_1_block_sums_device.argtypes = [vp, vp, vp, i32, i32, i32, vp]
         L.mat_mul_q4_0_q8_1_grouped_device.restype = i32
         L.mat_mul_q4_0_q8_1_grouped_device.argtypes = [vp, vp, vp, i32, vp, vp, i32, i32, i32, vp]
+        L.mat_mul_q4_0s_q8_1_grouped_device.restype = i32
+        L.mat_mul_q4_0s_q8_1_grouped_device.argtypes = [vp, vp, vp, i32, vp, vp, i32, i32, i32, vp]
         L.jjo_read_floor_device.restype = i32
         L.jjo_read_floor_device.argtypes = [vp, i64, vp, vp]
         L.linear_q4_0_workspace_bytes.restype = i64
@@ -167,6 +171,8 @@ def lib() -> ctypes.CDLL:
         L.moe_q4_0_ffn_workspace_bytes.argtypes = [i32, i32, i32, i32, i32]
         L.moe_q4_0_ffn_forward_device.restype = i32
         L.moe_q4_0_ffn_forward_device.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp, i64]
+        L.moe_q4_0s_ffn_forward_device.restype = i32
+        L.moe_q4_0s_ffn_forward_device.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, i32, vp, i64]
         L.q4_0_bytes.restype = i64
         L.q4_0_bytes.argtypes = [i64, i64]
         L.quantize_q4_0_host.restype = i32
@@ -354,8 +360,9 @@ def block_sums(w, xq, out, K: int, N: int, M: int, stream=None) -> None:
 
 
 def grouped_mat_mul(w, xq, expert_offsets, y, K: int, N: int, n_routes: int, route_dst=None,
-                    stream=None) -> None:
-    """One-launch MoE expert GEMM over routes sorted by expert (see the C header)."""
+                    stream=None, split: bool = False) -> None:
+    """One-launch MoE expert GEMM over routes sorted by expert (see the C header);
+    split: w holds the stacked experts repacked into the split layout."""
     import torch
     n_experts = expert_offsets.numel() - 1
     if expert_offsets.dtype != torch.int32:
@@ -365,9 +372,9 @@ def grouped_mat_mul(w, xq, expert_offsets, y, K: int, N: int, n_routes: int, rou
     if w.numel() * w.element_size() < n_experts * N * (K // QK) * Q4_BLOCK_BYTES:
         raise ValueError("weight buffer too small for all experts")
     rd = _dev(route_dst, "route_dst") if route_dst is not None else ctypes.c_void_p(0)
-    _check(lib().mat_mul_q4_0_q8_1_grouped_device(_dev(w, "w"), _dev(xq, "xq"), _dev(expert_offsets, "offsets"),
-                                                  n_experts, rd, _dev(y, "y"), K, N, n_routes,
-                                                  _stream(stream)), "grouped_mat_mul")
+    fn = lib().mat_mul_q4_0s_q8_1_grouped_device if split else lib().mat_mul_q4_0_q8_1_grouped_device
+    _check(fn(_dev(w, "w"), _dev(xq, "xq"), _dev(expert_offsets, "offsets"), n_experts, rd, _dev(y, "y"), K, N,
+              n_routes, _stream(stream)), "grouped_mat_mul")
 
 
 def read_floor(src, nbytes: int, out, stream=None) -> None:
@@ -471,9 +478,10 @@ def moe_ffn_workspace_bytes(num_tokens: int, hidden: int, inter: int, num_expert
 
 
 def moe_ffn(x, logits, w_gate, w_up, w_down, y, num_tokens: int, hidden: int, inter: int, num_experts: int,
-            top_k: int, ws, stream=None) -> None:
-    _check(lib().moe_q4_0_ffn_forward_device(_stream(stream), _dev(x, "x"), _dev(logits, "logits"),
-                                             _dev(w_gate, "w_gate"), _dev(w_up, "w_up"), _dev(w_down, "w_down"),
-                                             _dev(y, "y"), num_tokens, hidden, inter, num_experts, top_k,
-                                             _dev(ws, "ws"), ws.numel() * ws.element_size()),
-           "moe_q4_0_ffn_forward_device")
+            top_k: int, ws, stream=None, split: bool = False) -> None:
+    """The Q4_0 MoE FFN; split: the three expert weight buffers are in the split layout."""
+    fn = lib().moe_q4_0s_ffn_forward_device if split else lib().moe_q4_0_ffn_forward_device
+    _check(fn(_stream(stream), _dev(x, "x"), _dev(logits, "logits"), _dev(w_gate, "w_gate"), _dev(w_up, "w_up"),
+              _dev(w_down, "w_down"), _dev(y, "y"), num_tokens, hidden, inter, num_experts, top_k, _dev(ws, "ws"),
+              ws.numel() * ws.element_size()),
+           "moe_q4_0s_ffn_forward_device" if split else "moe_q4_0_ffn_forward_device")

@@ -507,6 +507,24 @@ int mat_mul_q4_0_q8_1_grouped_device(const void *d_w_q4_0, const void *d_x_q8_1,
     return JJO_OK;
 }
 
+int mat_mul_q4_0s_q8_1_grouped_device(const void *d_w_split, const void *d_x_q8_1,
+                                      const int32_t *d_expert_offsets, int n_experts,
+                                      const int32_t *d_route_dst, float *d_y, int ncols_k,
+                                      int nrows_out, int n_routes, void *stream) {
+    clear_error();
+    int rc = validate_split(d_w_split, d_x_q8_1, d_y, ncols_k, nrows_out, n_routes);
+    if (rc != JJO_OK) return rc;
+    if (d_expert_offsets == nullptr || n_experts <= 0 || n_experts > 4096)
+        return set_error(JJO_ERR_INVALID_ARG, "expert_offsets must be non-null and 1 <= n_experts <= 4096");
+    if ((rc = check_grouped_grid(n_routes, n_experts)) != JJO_OK) return rc;
+    if ((rc = require_gfx950()) != JJO_OK) return rc;
+    hipError_t e = launch_gemm_mfma_grouped(d_w_split, d_x_q8_1, d_expert_offsets, n_experts, d_route_dst,
+                                            d_y, ncols_k, nrows_out, n_routes, (hipStream_t)stream, nullptr, 0,
+                                            true);
+    if (e != hipSuccess) return hip_fail(e, "grouped gemm (split layout) launch");
+    return JJO_OK;
+}
+
 int mat_mul_q4_0_q8_1(const void *weight_q4_0, const float *input, uint8_t *quant_workspace,
                       float *output, const int64_t *dims, int ndims, int nrows_out, int ncols_k) {
     clear_error();
@@ -884,10 +902,13 @@ int64_t moe_q4_0_ffn_workspace_bytes(int num_tokens, int hidden_size, int interm
     return moe_ws_layout(nullptr, num_tokens, hidden_size, intermediate_size, num_experts, top_k).bytes;
 }
 
-int moe_q4_0_ffn_forward_device(void *stream, const float *x, const float *logits, const void *w_gate,
-                                const void *w_up, const void *w_down, float *y, int num_tokens, int hidden_size,
-                                int intermediate_size, int num_experts, int top_k, void *workspace,
-                                int64_t workspace_bytes) {
+}  // extern "C"
+
+namespace {
+// The Q4_0 MoE FFN; split: the three expert weight buffers are in the split layout.
+int moe_ffn_run(bool split, void *stream, const float *x, const float *logits, const void *w_gate, const void *w_up,
+                const void *w_down, float *y, int num_tokens, int hidden_size, int intermediate_size, int num_experts,
+                int top_k, void *workspace, int64_t workspace_bytes) {
     clear_error();
     const int T = num_tokens, H = hidden_size, I = intermediate_size, E = num_experts;
     int rc = check_moe_shape(T, H, I, E, top_k);
@@ -895,9 +916,11 @@ int moe_q4_0_ffn_forward_device(void *stream, const float *x, const float *logit
     if (x == nullptr || logits == nullptr || w_gate == nullptr || w_up == nullptr || w_down == nullptr ||
         y == nullptr || workspace == nullptr)
         return set_error(JJO_ERR_INVALID_ARG, "moe_ffn: null pointer argument");
-    if (!aligned(x, 16) || !aligned(y, 16) || !aligned(workspace, 256) || !aligned(w_gate, 4) ||
-        !aligned(w_up, 4) || !aligned(w_down, 4))
-        return set_error(JJO_ERR_INVALID_ARG, "moe_ffn: x, y 16-byte, workspace 256-byte, weights 4-byte aligned");
+    const int wal = split ? 16 : 4;
+    if (!aligned(x, 16) || !aligned(y, 16) || !aligned(workspace, 256) || !aligned(w_gate, wal) ||
+        !aligned(w_up, wal) || !aligned(w_down, wal))
+        return set_error(JJO_ERR_INVALID_ARG, "moe_ffn: x, y 16-byte, workspace 256-byte, weights %d-byte aligned",
+                         wal);
     const MoeWs ws = moe_ws_layout((uint8_t *)workspace, T, H, I, E, top_k);
     if (workspace_bytes < ws.bytes)
         return set_error(JJO_ERR_INVALID_ARG, "moe_ffn: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
@@ -916,14 +939,35 @@ int moe_q4_0_ffn_forward_device(void *stream, const float *x, const float *logit
         return hip_fail(e, "moe_ffn gather");
     // 4) gate|up of every route's expert in one grouped launch whose epilogue applies
     //    SwiGLU and writes the Q8_1 input of the down projection (no fp32 gate|up)
-    if ((e = launch_gemm_gate_up_swiglu_q8_1(w_gate, w_up, ws.xp, ws.offsets, E, ws.midq, H, I, R, s)) != hipSuccess)
+    if ((e = launch_gemm_gate_up_swiglu_q8_1(w_gate, w_up, ws.xp, ws.offsets, E, ws.midq, H, I, R, s, split)) !=
+        hipSuccess)
         return hip_fail(e, "moe_ffn gate_up_swiglu");
-    // 6) down projection, 7) weighted combine back to token order
-    if ((e = launch_gemm_mfma_grouped(w_down, ws.midq, ws.offsets, E, nullptr, ws.eout, I, H, R, s)) != hipSuccess)
+    // 5) down projection, 6) weighted combine back to token order
+    if ((e = launch_gemm_mfma_grouped(w_down, ws.midq, ws.offsets, E, nullptr, ws.eout, I, H, R, s, nullptr, 0,
+                                      split)) != hipSuccess)
         return hip_fail(e, "moe_ffn down");
     if ((e = launch_moe_combine(ws.eout, ws.dst_of_route, ws.route_w, y, T, H, top_k, s)) != hipSuccess)
         return hip_fail(e, "moe_ffn combine");
     return JJO_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int moe_q4_0_ffn_forward_device(void *stream, const float *x, const float *logits, const void *w_gate,
+                                const void *w_up, const void *w_down, float *y, int num_tokens, int hidden_size,
+                                int intermediate_size, int num_experts, int top_k, void *workspace,
+                                int64_t workspace_bytes) {
+    return moe_ffn_run(false, stream, x, logits, w_gate, w_up, w_down, y, num_tokens, hidden_size,
+                       intermediate_size, num_experts, top_k, workspace, workspace_bytes);
+}
+
+int moe_q4_0s_ffn_forward_device(void *stream, const float *x, const float *logits, const void *w_gate_split,
+                                 const void *w_up_split, const void *w_down_split, float *y, int num_tokens,
+                                 int hidden_size, int intermediate_size, int num_experts, int top_k, void *workspace,
+                                 int64_t workspace_bytes) {
+    return moe_ffn_run(true, stream, x, logits, w_gate_split, w_up_split, w_down_split, y, num_tokens, hidden_size,
+                       intermediate_size, num_experts, top_k, workspace, workspace_bytes);
 }
 
 }  // extern "C"

@@ -73,7 +73,11 @@ constexpr int kXRuns = kXUnits / 64;                     // 18 wave-sized (1 KB)
 // silu(gate) * up for those 64 intermediate values of each route to `midq`
 // (superblock-major over the M routes, as the quantizer lays out a [M][n_split]
 // activation).  n_split is the intermediate size I.
-template <bool kGrouped, bool kSwiglu = false>
+// kSplit: the weights are in the split layout (a nibble plane, then an fp16 scale
+// plane, over all rows of the buffer: the stacked experts of a grouped launch, each
+// of w and w2 on its own); the staging thread's two blocks are then 32 contiguous
+// nibble bytes and one scale dword, the same three loads and nine registers.
+template <bool kGrouped, bool kSwiglu = false, bool kSplit = false>
 __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     const uint8_t *__restrict__ w_all, const uint8_t *__restrict__ xq, float *__restrict__ y, int K,
     int N, int M, const int32_t *__restrict__ expert_offsets, int n_experts,
@@ -157,18 +161,54 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
         }
         w_src = w + (size_t)min(n_loc0 + st_row, n_mat - 1) * row_bytes + (size_t)st_half * 36;
     }
+    // Split layout: the same rows, as (matrix, row of its buffer, rows of its buffer).
+    const uint8_t *wq_s = nullptr, *wd_s = nullptr;
+    if constexpr (kSplit) {
+        const int nb_ = K / kQK;
+        const uint8_t *mat;
+        int64_t rows_total, row;
+        if constexpr (kSwiglu) {
+            const int ni0 = blockIdx.x * 64;
+            mat = st_row < 64 ? w_all : w2;
+            rows_total = (int64_t)n_experts * n_split;
+            row = (int64_t)expert * n_split + min(ni0 + (st_row & 63), n_split - 1);
+        } else {
+            if (kGrouped && w2 != nullptr) {
+                const bool first = n0 < n_split;
+                const int rows_e = first ? n_split : N - n_split;
+                mat = first ? w_all : w2;
+                rows_total = (int64_t)n_experts * rows_e;
+                row = (int64_t)expert * rows_e + min((first ? n0 : n0 - n_split) + st_row, rows_e - 1);
+            } else {
+                mat = w_all;
+                rows_total = kGrouped ? (int64_t)n_experts * N : N;
+                row = (kGrouped ? (int64_t)expert * N : 0) + min(n0 + st_row, N - 1);
+            }
+        }
+        wq_s = mat + ((size_t)row * nb_ + 2 * st_half) * 16;
+        wd_s = mat + (size_t)rows_total * nb_ * 16 + ((size_t)row * nb_ + 2 * st_half) * 2;
+    }
     // This thread's 2 raw Q4_0 blocks (36 bytes) of a stage, in two register sets:
     // stage k lands in set k & 1, two compute phases before it is unpacked.
     uint32_t wr0[9], wr1[9];
 
     // Three vector-memory instructions per call (the explicit waits count on it).
     auto load_w = [&](int c, uint32_t(&wst)[9]) {
-        const uint8_t *p = w_src + (size_t)c * (KB * kQ4BlockBytes);
-        const u32x4a4 a = *reinterpret_cast<const u32x4a4 *>(p);
-        const u32x4a4 b = *reinterpret_cast<const u32x4a4 *>(p + 16);
-        wst[0] = a.x; wst[1] = a.y; wst[2] = a.z; wst[3] = a.w;
-        wst[4] = b.x; wst[5] = b.y; wst[6] = b.z; wst[7] = b.w;
-        wst[8] = *reinterpret_cast<const uint32_t *>(p + 32);
+        if constexpr (kSplit) {
+            const uint8_t *pq = wq_s + (size_t)c * (KB * 16);
+            const u32x4 a = *reinterpret_cast<const u32x4 *>(pq);
+            const u32x4 b = *reinterpret_cast<const u32x4 *>(pq + 16);
+            wst[0] = a.x; wst[1] = a.y; wst[2] = a.z; wst[3] = a.w;
+            wst[4] = b.x; wst[5] = b.y; wst[6] = b.z; wst[7] = b.w;
+            wst[8] = *reinterpret_cast<const uint32_t *>(wd_s + (size_t)c * (KB * 2));
+        } else {
+            const uint8_t *p = w_src + (size_t)c * (KB * kQ4BlockBytes);
+            const u32x4a4 a = *reinterpret_cast<const u32x4a4 *>(p);
+            const u32x4a4 b = *reinterpret_cast<const u32x4a4 *>(p + 16);
+            wst[0] = a.x; wst[1] = a.y; wst[2] = a.z; wst[3] = a.w;
+            wst[4] = b.x; wst[5] = b.y; wst[6] = b.z; wst[7] = b.w;
+            wst[8] = *reinterpret_cast<const uint32_t *>(p + 32);
+        }
     };
 
     // Activation tile of stage c = superblock c: tokens m0.. of one contiguous run.
@@ -217,7 +257,11 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
             // dwords 5..8.
             uint32_t q[4];
             uint32_t dbits;
-            if (i == 0) {
+            if constexpr (kSplit) {  // nibbles of block i in dwords 4i..4i+3, both scales in dword 8
+                dbits = i == 0 ? (wst[8] & 0xffffu) : (wst[8] >> 16);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) q[k] = wst[4 * i + k];
+            } else if (i == 0) {
                 dbits = wst[0] & 0xffffu;
 #pragma unroll
                 for (int k = 0; k < 4; ++k) q[k] = __builtin_amdgcn_alignbyte(wst[k + 1], wst[k], 2);
@@ -671,9 +715,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
     }
 }
 
-template <bool kGrouped, bool kSwiglu = false>
+template <bool kGrouped, bool kSwiglu = false, bool kSplit = false>
 hipError_t set_smem_attr() {
-    return ensure_dynamic_lds((const void *)gemm_q4_0_q8_1_mfma_kernel<kGrouped, kSwiglu>, kSmemBytes);
+    return ensure_dynamic_lds((const void *)gemm_q4_0_q8_1_mfma_kernel<kGrouped, kSwiglu, kSplit>, kSmemBytes);
 }
 static_assert(BM * (BN + 4) * 4 <= kSmemBytes, "fused SwiGLU result tile fits the staging LDS");
 
@@ -692,29 +736,41 @@ hipError_t launch_gemm_mfma(const void *w, const void *xq, float *y, int K, int 
 
 hipError_t launch_gemm_mfma_grouped(const void *w, const void *xq, const int32_t *expert_offsets,
                                     int n_experts, const int32_t *route_dst, float *y, int K,
-                                    int N, int n_routes, hipStream_t stream, const void *w2, int n_split) {
-    hipError_t e = set_smem_attr<true>();
+                                    int N, int n_routes, hipStream_t stream, const void *w2, int n_split,
+                                    bool split) {
+    hipError_t e = split ? set_smem_attr<true, false, true>() : set_smem_attr<true>();
     if (e != hipSuccess) return e;
     // Upper bound on the number of token tiles over all experts.
     const int max_tiles = (n_routes + BM - 1) / BM + n_experts;
     const dim3 grid((N + BN - 1) / BN, max_tiles);
-    hipLaunchKernelGGL(gemm_q4_0_q8_1_mfma_kernel<true>, grid, dim3(kThreads), kSmemBytes, stream,
-                       (const uint8_t *)w, (const uint8_t *)xq, y, K, N, n_routes, expert_offsets,
-                       n_experts, route_dst, (const uint8_t *)w2, n_split);
+    if (split)
+        hipLaunchKernelGGL((gemm_q4_0_q8_1_mfma_kernel<true, false, true>), grid, dim3(kThreads), kSmemBytes,
+                           stream, (const uint8_t *)w, (const uint8_t *)xq, y, K, N, n_routes, expert_offsets,
+                           n_experts, route_dst, (const uint8_t *)w2, n_split, (uint8_t *)nullptr);
+    else
+        hipLaunchKernelGGL(gemm_q4_0_q8_1_mfma_kernel<true>, grid, dim3(kThreads), kSmemBytes, stream,
+                           (const uint8_t *)w, (const uint8_t *)xq, y, K, N, n_routes, expert_offsets,
+                           n_experts, route_dst, (const uint8_t *)w2, n_split);
     return hipGetLastError();
 }
 
 hipError_t launch_gemm_gate_up_swiglu_q8_1(const void *w_gate, const void *w_up, const void *xq,
                                            const int32_t *expert_offsets, int n_experts, void *mid_q8_1, int K,
-                                           int I, int n_routes, hipStream_t stream) {
-    hipError_t e = set_smem_attr<true, true>();
+                                           int I, int n_routes, hipStream_t stream, bool split) {
+    hipError_t e = split ? set_smem_attr<true, true, true>() : set_smem_attr<true, true>();
     if (e != hipSuccess) return e;
     const int max_tiles = (n_routes + BM - 1) / BM + n_experts;
     const dim3 grid(I / 64, max_tiles);
-    hipLaunchKernelGGL((gemm_q4_0_q8_1_mfma_kernel<true, true>), grid, dim3(kThreads), kSmemBytes, stream,
-                       (const uint8_t *)w_gate, (const uint8_t *)xq, (float *)nullptr, K, 2 * I, n_routes,
-                       expert_offsets, n_experts, (const int32_t *)nullptr, (const uint8_t *)w_up, I,
-                       (uint8_t *)mid_q8_1);
+    if (split)
+        hipLaunchKernelGGL((gemm_q4_0_q8_1_mfma_kernel<true, true, true>), grid, dim3(kThreads), kSmemBytes, stream,
+                           (const uint8_t *)w_gate, (const uint8_t *)xq, (float *)nullptr, K, 2 * I, n_routes,
+                           expert_offsets, n_experts, (const int32_t *)nullptr, (const uint8_t *)w_up, I,
+                           (uint8_t *)mid_q8_1);
+    else
+        hipLaunchKernelGGL((gemm_q4_0_q8_1_mfma_kernel<true, true>), grid, dim3(kThreads), kSmemBytes, stream,
+                           (const uint8_t *)w_gate, (const uint8_t *)xq, (float *)nullptr, K, 2 * I, n_routes,
+                           expert_offsets, n_experts, (const int32_t *)nullptr, (const uint8_t *)w_up, I,
+                           (uint8_t *)mid_q8_1);
     return hipGetLastError();
 }
 

@@ -76,12 +76,12 @@ hipError_t launch_gemm_mfma(const void *w, const void *xq, float *y, int K, int 
 hipError_t launch_gemm_mfma_grouped(const void *w, const void *xq, const int32_t *expert_offsets,
                                     int n_experts, const int32_t *route_dst, float *y, int K,
                                     int N, int n_routes, hipStream_t stream, const void *w2 = nullptr,
-                                    int n_split = 0);
+                                    int n_split = 0, bool split = false);
 // gate|up grouped GEMM with the SwiGLU + Q8_1 quantize epilogue: writes the Q8_1
 // bytes of silu(x.W_gate) * (x.W_up) per route (I % 128 == 0) and nothing else.
 hipError_t launch_gemm_gate_up_swiglu_q8_1(const void *w_gate, const void *w_up, const void *xq,
                                            const int32_t *expert_offsets, int n_experts, void *mid_q8_1, int K,
-                                           int I, int n_routes, hipStream_t stream);
+                                           int I, int n_routes, hipStream_t stream, bool split = false);
 hipError_t launch_swiglu_quantize_q8_1(const float *gate_up, void *y, float *mid_out, int64_t K, int64_t rows,
                                        hipStream_t stream);
 hipError_t launch_moe_top_k(const float *logits, float *weights, int *ids, int num_tokens, int num_experts,

@@ -362,3 +362,60 @@ def test_moe_ffn_rejects_small_workspace(dev):
     y = torch.empty(T * H, dtype=torch.float32, device=dev)
     with pytest.raises(RuntimeError, match="workspace"):
         capi.moe_ffn(z, z, z, z, z, y, T, H, I, E, k, ws)
+
+
+# ------------------------------------------------------------------ split-layout experts
+def _split_stack(w_dev, rows, K, dev):
+    """The stacked expert matrices repacked into the split layout as one matrix."""
+    import torch
+    out = torch.empty_like(w_dev)
+    capi.q4_0_to_split(w_dev, out, rows, K)
+    return out
+
+
+@pytest.mark.parametrize("counts,N", [([1, 129, 0, 31, 160, 32, 33, 7], 256), ([3, 2, 1, 4], 384),
+                                      ([200, 0, 5], 300)])
+def test_grouped_split_layout(counts, N, dev):
+    """The grouped GEMM on split-layout experts equals the block_q4_0 launch bit for
+    bit (the same kernel and arithmetic; only the weight loads differ), with route
+    scatter, empty experts, narrow and paired tails and a ragged N."""
+    import torch
+    E, K = len(counts), 512
+    note(f"grouped split counts={counts} N={N}")
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    R = int(offsets[-1])
+    rng = np.random.default_rng(R + N)
+    xq = c_oracle.quantize_q8_1(rng.standard_normal((R, K)).astype(np.float32), [K, R])
+    w = to_dev(np.concatenate([make_w(N, K, rng) for _ in range(E)]), dev)
+    ws = _split_stack(w, E * N, K, dev)
+    dst = to_dev(rng.permutation(R).astype(np.int32), dev)
+    off_d, xq_d = to_dev(offsets, dev), to_dev(xq, dev)
+    y1 = torch.full((R * N,), float("nan"), dtype=torch.float32, device=dev)
+    y2 = torch.full((R * N,), float("nan"), dtype=torch.float32, device=dev)
+    capi.grouped_mat_mul(w, xq_d, off_d, y1, K, N, R, route_dst=dst)
+    capi.grouped_mat_mul(ws, xq_d, off_d, y2, K, N, R, route_dst=dst, split=True)
+    a, b = host(y1), host(y2)
+    assert not np.isnan(a).any()
+    assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("T,H,I,E,top_k", MOE_CASES)
+def test_moe_ffn_split_layout(T, H, I, E, top_k, dev):
+    """The FFN on split-layout expert weights equals the block_q4_0 FFN bit for bit."""
+    import torch
+    note(f"moe_ffn split T={T} H={H} I={I} E={E} k={top_k}")
+    x, lg, wg, wu, wd = _ffn_inputs(T, H, I, E, 900 + T)
+    d = {k: to_dev(v, dev) for k, v in dict(x=x, lg=lg, wg=np.concatenate(wg), wu=np.concatenate(wu),
+                                          wd=np.concatenate(wd)).items()}
+    sg = _split_stack(d["wg"], E * I, H, dev)
+    su = _split_stack(d["wu"], E * I, H, dev)
+    sd = _split_stack(d["wd"], E * H, I, dev)
+    ws = torch.empty(capi.moe_ffn_workspace_bytes(T, H, I, E, top_k), dtype=torch.uint8, device=dev)
+    y1 = torch.full((T * H,), float("nan"), dtype=torch.float32, device=dev)
+    y2 = torch.full((T * H,), float("nan"), dtype=torch.float32, device=dev)
+    capi.moe_ffn(d["x"], d["lg"], d["wg"], d["wu"], d["wd"], y1, T, H, I, E, top_k, ws)
+    capi.moe_ffn(d["x"], d["lg"], sg, su, sd, y2, T, H, I, E, top_k, ws, split=True)
+    a, b = host(y1), host(y2)
+    assert np.isfinite(a).all()
+    assert np.array_equal(a, b)
+
