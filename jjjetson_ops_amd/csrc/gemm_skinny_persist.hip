@@ -35,7 +35,8 @@
 //
 // SPLIT: weights in the split layout (nibble plane + fp16 scale plane).  An item
 // is then the 16 rows' 8 nibble blocks (16 x 128 bytes, gathered by two DMA
-// instructions) followed by their 16 x 8 scales (one DMA instruction of 16 lanes):
+// instructions; block j of row r in slot j ^ (r & 7) of the row, against LDS bank
+// conflicts) followed by their 16 x 8 scales (one DMA instruction of 16 lanes):
 // the same 2304 bytes and three DMA instructions, and every operand read aligned.
 //
 // Requirements (checked by the launcher): M <= 16, K % 256 == 0, w and xq 16-byte aligned.
@@ -136,8 +137,13 @@ __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uin
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
                     const int c = 64 * i + lane;
-                    const int r = min((tile0 + t) * 16 + (c >> 3), N - 1);
-                    dma16(w + ((size_t)r * nb + blk0 + (c & 7)) * 16, (uint32_t)(uintptr_t)(slot + 1024 * i));
+                    // Slot (row c / 8, j = c % 8) holds block j ^ (row & 7) of that row: with
+                    // 128-byte rows, the 16 lanes reading one block of 16 rows would
+                    // otherwise all hit one LDS bank.
+                    const int rr = c >> 3;
+                    const int r = min((tile0 + t) * 16 + rr, N - 1);
+                    dma16(w + ((size_t)r * nb + blk0 + ((c & 7) ^ (rr & 7))) * 16,
+                          (uint32_t)(uintptr_t)(slot + 1024 * i));
                 }
                 if (lane < 16) {
                     const int r = min((tile0 + t) * 16 + lane, N - 1);
@@ -261,7 +267,8 @@ __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uin
                     uint32_t q0, q1;
                     _Float16 dw;
                     if constexpr (SPLIT) {
-                        const uint2 qq = *reinterpret_cast<const uint2 *>(wq_s + (2 * p + po) * 16 + 8 * kc);
+                        const uint2 qq =
+                            *reinterpret_cast<const uint2 *>(wq_s + ((2 * p + po) ^ (l16 & 7)) * 16 + 8 * kc);
                         q0 = qq.x;
                         q1 = qq.y;
                         dw = wd_s[2 * p + po];
@@ -356,7 +363,7 @@ __global__ __launch_bounds__(64 * kPW) void gemm_skinny_persist_kernel(const uin
                     uint32_t q;
                     _Float16 dw;
                     if constexpr (SPLIT) {
-                        q = *reinterpret_cast<const uint32_t *>(wq_s + bb * 16 + 4 * g);
+                        q = *reinterpret_cast<const uint32_t *>(wq_s + (bb ^ (l16 & 7)) * 16 + 4 * g);
                         dw = wd_s[bb];
                     } else {
                         const uint8_t *wr = wr0 + bb * kQ4BlockBytes;
