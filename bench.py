@@ -450,6 +450,9 @@ def main():
         ("m4_k4096_n14336", 4, 4096, 14336, 2, args.steps),
         ("m8_k4096_n14336", 8, 4096, 14336, 2, args.steps),
         ("m16_k4096_n14336", 16, 4096, 14336, 2, args.steps),
+        ("m4_k4096_n14336_split", 4, 4096, 14336, 2, args.steps),
+        ("m8_k4096_n14336_split", 8, 4096, 14336, 2, args.steps),
+        ("m16_k4096_n14336_split", 16, 4096, 14336, 2, args.steps),
         ("prefill_m2048_k4096_n4096", 2048, 4096, 4096, 3, max(20, args.steps // 4)),
         ("prefill_m2048_k4096_n14336", 2048, 4096, 14336, 3, max(20, args.steps // 4)),
         ("prefill_m2048_k4096_n4096_split", 2048, 4096, 4096, 3, max(20, args.steps // 4)),
