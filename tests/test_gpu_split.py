@@ -128,7 +128,10 @@ def test_split_f32_batch(M, dev):
 
 @pytest.mark.parametrize("K,N,M", [(4096, 256, 128), (4096, 300, 130), (384, 64, 257), (128, 96, 9),
                                    (11008, 128, 64), (512, 4100, 96), (4096, 257, 5), (4096, 1000, 8),
-                                   (11264, 77, 12), (256, 33, 16), (4096, 14336, 16), (4096, 70, 17)])
+                                   (11264, 77, 12), (256, 33, 16), (4096, 14336, 16), (4096, 70, 17),
+                                   # K % 256 != 0: the skinny kernel is unsupported, batch 3/6 take
+                                   # the GEMV (two K slices), batch 12 the GEMM
+                                   (4224, 100, 3), (4224, 100, 6), (4224, 100, 12)])
 def test_split_gemm(K, N, M, dev):
     import torch
     note(f"split gemm M={M} K={K} N={N}")
