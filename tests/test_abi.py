@@ -136,3 +136,47 @@ def test_pybind_rejects_bad_buffers():
         mm_q4_0_q8_1_me.mmq(w, x, np.zeros(288, np.uint8), np.zeros(16, np.float64), [128, 2, 1, 1], 8, 128)
     with pytest.raises(ValueError):  # dims[0] != ncols_k
         mm_q4_0_q8_1_me.mmq(w, x, np.zeros(288, np.uint8), np.zeros(16, np.float32), [128, 2, 1, 1], 8, 256)
+
+
+def test_newer_device_entries_validate_before_touching_a_device():
+    """Every device entry beyond the reference's pair rejects a malformed call with
+    JJO_ERR_INVALID_ARG before it looks for a GPU (checked here, with none)."""
+    L = capi.lib()
+    P = ctypes.c_void_p
+    a16, a8 = P(16), P(8)
+    bad = capi.JJO_ERR_INVALID_ARG
+    calls = {
+        # split layout: weight must be 16-byte aligned; K a multiple of 128
+        "mat_mul_q4_0s_q8_1_device": lambda: L.mat_mul_q4_0s_q8_1_device(a8, a16, a16, 128, 4, 1, None),
+        "mat_mul_q4_0s_q8_1_f32_device": lambda: L.mat_mul_q4_0s_q8_1_f32_device(a16, a16, a16, a16, 96, 4, 1,
+                                                                                  None),
+        "mat_mul_q4_0s_q8_1_grouped_device": lambda: L.mat_mul_q4_0s_q8_1_grouped_device(
+            a16, a16, None, 8, None, a16, 128, 4, 4, None),
+        "q4_0_to_split_device": lambda: L.q4_0_to_split_device(a16, a16, 4, 100, None),
+        # engine linear layers: in_features a multiple of 128, sizes positive
+        "linear_q4_0_forward_device": lambda: L.linear_q4_0_forward_device(None, a16, a16, a16, a16, 96, 4, 1),
+        "linear_q4_0s_forward_device": lambda: L.linear_q4_0s_forward_device(None, a16, a16, a16, a16, 128, 0, 1),
+        "linear_q4_0_forward_device_noalloc": lambda: L.linear_q4_0_forward_device_noalloc(
+            None, a16, a16, a16, 4096, 4, 1 << 20),
+        # MoE stages
+        "moe_top_k_device": lambda: L.moe_top_k_device(None, a16, a16, a16, 4, 8, 0),
+        "moe_dispatch_q8_1_device": lambda: L.moe_dispatch_q8_1_device(None, a16, None, 4, 0, 128, 8, a16, a16,
+                                                                       a16, None),
+        "moe_q4_0_gate_up_device": lambda: L.moe_q4_0_gate_up_device(None, a16, a16, a16, a16, 8, a16, 128, 100,
+                                                                     4),
+        "moe_q4_0_gate_up_swiglu_q8_1_device": lambda: L.moe_q4_0_gate_up_swiglu_q8_1_device(
+            None, a16, a16, a16, a16, 8, a16, 128, 100, 4),
+        "swiglu_quantize_q8_1_device": lambda: L.swiglu_quantize_q8_1_device(None, a16, a16, None, 4, 100),
+        "moe_combine_device": lambda: L.moe_combine_device(None, a16, a16, a16, a16, 4, 6, 2),
+        "moe_q4_0_ffn_forward_device": lambda: L.moe_q4_0_ffn_forward_device(
+            None, a16, a16, a16, a16, a16, a16, 4, 128, 128, 8, 2, P(256), 16),
+        "moe_q4_0s_ffn_forward_device": lambda: L.moe_q4_0s_ffn_forward_device(
+            None, a16, a16, a8, a16, a16, a16, 4, 128, 128, 8, 2, P(256), 1 << 30),
+        # weights and diagnostics
+        "quantize_q4_0_device": lambda: L.quantize_q4_0_device(None, a16, a16, 4, 100),
+        "jjo_read_floor_device": lambda: L.jjo_read_floor_device(a16, -1, a16, None),
+    }
+    for name, call in calls.items():
+        rc = call()
+        assert rc == bad, f"{name}: rc {rc}, last error {L.jjo_last_error()!r}"
+        assert L.jjo_last_error(), name
