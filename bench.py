@@ -465,6 +465,8 @@ def main():
             res = time_moe(dev, max(10, args.steps // 10), 3)
         elif args.only == "moe_ffn":
             res = time_moe_ffn(dev, max(5, args.steps // 20), 2)
+        elif args.only == "moe_ffn_split":
+            res = time_moe_ffn(dev, max(5, args.steps // 20), 2, split=True)
         elif args.only == "read_floor":
             res = time_read_floor(dev, args.steps, args.warmup)
         elif args.only == "quantize_q4_0":
