@@ -118,6 +118,9 @@ MOE_CASES = [  # T, H, I, E, top_k
     (64, 256, 384, 8, 2),
     (5, 128, 128, 4, 1),
     (300, 512, 256, 16, 4),
+    (64, 256, 256, 64, 8),     # many experts, top-8: mostly short (narrow / paired) tiles
+    (40, 128, 128, 256, 8),    # 256 experts for 320 routes: most get 0..3
+    (33, 1024, 384, 8, 2),     # wider hidden size
 ]
 
 
