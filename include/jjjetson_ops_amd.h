@@ -356,7 +356,8 @@ int moe_combine_device(void *stream, const float *expert_out, const int32_t *dst
 /*
  * The whole Q4_0 MoE FFN on device pointers: x fp32 [T][H], logits fp32 [T][E],
  * y fp32 [T][H].  `workspace` (256-byte aligned) holds every intermediate; its
- * size is moe_q4_0_ffn_workspace_bytes(...).  Eight launches, no allocation,
+ * size is moe_q4_0_ffn_workspace_bytes(...).  Seven launches (quantize x, top-k,
+ * dispatch, gather, gate|up with SwiGLU and Q8_1, down, combine), no allocation,
  * asynchronous on `stream`.  H % 128 == 0, I % 128 == 0.
  */
 int64_t moe_q4_0_ffn_workspace_bytes(int num_tokens, int hidden_size, int intermediate_size, int num_experts,
