@@ -75,3 +75,38 @@ def test_graph_moe_ffn(dev):
     ws = torch.empty(capi.moe_ffn_workspace_bytes(T, H, I, E, k), dtype=torch.uint8, device=dev)
     y = torch.empty(T * H, dtype=torch.float32, device=dev)
     _replays_match(lambda: capi.moe_ffn(x, lg, wg, wu, wd, y, T, H, I, E, k, ws), [y], dev)
+
+
+@pytest.mark.parametrize("M", [1, 5, 16, 200])
+def test_graph_split_layout_matmul_f32(M, dev):
+    """The split-layout entries in a graph: the fused decode step (the headline path),
+    the skinny kernel and the MFMA GEMM."""
+    import torch
+    note(f"graph split mat_mul_f32 M={M}")
+    K, N = 1024, 384
+    rng = np.random.default_rng(100 + M)
+    w = torch.from_numpy(_w(N, K, rng)).to(dev)
+    ws = torch.empty_like(w)
+    capi.q4_0_to_split(w, ws, N, K)
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(dev)
+    xq = torch.empty(capi.q8_1_output_bytes([K, M]), dtype=torch.uint8, device=dev)
+    y = torch.empty(M * N, dtype=torch.float32, device=dev)
+    _replays_match(lambda: capi.mat_mul_split_f32(ws, x, xq, y, K, N, M), [y, xq], dev)
+
+
+def test_graph_moe_ffn_split_layout(dev):
+    import torch
+    note("graph moe_ffn split")
+    T, H, I, E, k = 48, 256, 256, 8, 2
+    rng = np.random.default_rng(19)
+    mats = []
+    for rows, cols in ((I, H), (I, H), (H, I)):
+        w = torch.from_numpy(np.concatenate([_w(rows, cols, rng) for _ in range(E)])).to(dev)
+        s = torch.empty_like(w)
+        capi.q4_0_to_split(w, s, E * rows, cols)
+        mats.append(s)
+    x = torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)).to(dev)
+    lg = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float32)).to(dev)
+    wsp = torch.empty(capi.moe_ffn_workspace_bytes(T, H, I, E, k), dtype=torch.uint8, device=dev)
+    y = torch.empty(T * H, dtype=torch.float32, device=dev)
+    _replays_match(lambda: capi.moe_ffn(x, lg, *mats, y, T, H, I, E, k, wsp, split=True), [y], dev)
