@@ -21,6 +21,10 @@ CASES = [  # (K, N, M, algo)
     (4096, 1024, 16, capi.ALGO_SKINNY_LDS),
     (2048, 1024, 256, capi.ALGO_MFMA),
     (1024, 640, 100, capi.ALGO_AUTO),
+    # split-layout weights (AUTO over the split kernels: GEMV, skinny, GEMM)
+    (4096, 512, 1, "split"),
+    (4096, 1024, 8, "split"),
+    (2048, 512, 200, "split"),
 ]
 data = []
 for K, N, M, algo in CASES:
@@ -29,7 +33,12 @@ for K, N, M, algo in CASES:
     x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(dev)
     xq = torch.empty(capi.q8_1_output_bytes([K, M]), dtype=torch.uint8, device=dev)
     capi.quantize_q8_1(x, xq, [K, M])
-    data.append((w.to(dev), xq))
+    w = w.to(dev)
+    if algo == "split":
+        ws = torch.empty_like(w)
+        capi.q4_0_to_split(w, ws, N, K)
+        w = ws
+    data.append((w, xq))
 torch.cuda.synchronize()
 
 # Threads start together; each one's first call is also the process's first call of
@@ -48,7 +57,10 @@ def worker(i):
         with torch.cuda.stream(s):
             for _ in range(20):
                 y = torch.empty(M * N, dtype=torch.float32, device=dev)
-                capi.mat_mul(w, xq, y, K, N, M, algo=algo, stream=s)
+                if algo == "split":
+                    capi.mat_mul_split(w, xq, y, K, N, M, stream=s)
+                else:
+                    capi.mat_mul(w, xq, y, K, N, M, algo=algo, stream=s)
                 outs.append(y)
         s.synchronize()
         results[i] = [o.cpu() for o in outs]
@@ -66,7 +78,10 @@ if errors:
 for i, (K, N, M, algo) in enumerate(CASES):
     w, xq = data[i]
     y = torch.empty(M * N, dtype=torch.float32, device=dev)
-    capi.mat_mul(w, xq, y, K, N, M, algo=algo)
+    if algo == "split":
+        capi.mat_mul_split(w, xq, y, K, N, M)
+    else:
+        capi.mat_mul(w, xq, y, K, N, M, algo=algo)
     torch.cuda.synchronize()
     ref = y.cpu()
     for r, o in enumerate(results[i]):
