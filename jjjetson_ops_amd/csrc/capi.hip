@@ -176,8 +176,16 @@ int run_mm(const void *w, const void *xq, float *y, int K, int N, int M, int alg
             algo = JJO_ALGO_GEMV;
         // The 128 x 128 tiles fill the chip only from about 1.5 tiles per CU; below
         // that the 64 x 64 kernel runs four times as many workgroups and is up to 2x
-        // faster (K=4096: N=14336 up to M=384, N=4096 up to M=1024).
-        else if (2 * (int64_t)((N + 127) / 128) * ((M + 127) / 128) < 3 * (int64_t)device_cus())
+        // faster (K=4096: N=14336 up to M=384, N=4096 up to M=1024).  Above it the
+        // 128 x 128 kernel also needs its rounds (two workgroups per CU) well filled:
+        // 80% over one or two rounds, 70% over more.  N=11008, M=768 is 516 tiles, a
+        // second round for 4 of them (156 us against 128 us for the 64 x 64 kernel);
+        // 896 tiles (N=14336, M=1024, 88%) stay on it (198 against 213 us), and so do
+        // 1120 (M=1280, three rounds 73% full: 238 against 258 us).
+        else if (const int64_t t128 = (int64_t)((N + 127) / 128) * ((M + 127) / 128),
+                 slots = 2 * (int64_t)device_cus(), rounds = (t128 + slots - 1) / slots;
+                 2 * t128 < 3 * (int64_t)device_cus() ||
+                 (rounds <= 2 ? 5 * t128 < 4 * slots * rounds : 10 * t128 < 7 * slots * rounds))
             // Down to 1.5 workgroups of 64 x 64 per CU, 32-row tiles (twice the
             // workgroups, each wave half of a stage's blocks) are 7-20% faster still.
             algo = 2 * (int64_t)((N + 63) / 64) * ((M + 63) / 64) <= 3 * (int64_t)device_cus() ? JJO_ALGO_MFMA32
