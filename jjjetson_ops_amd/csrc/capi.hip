@@ -158,6 +158,26 @@ int check_grouped_grid(int n_routes, int n_experts) {
     return JJO_OK;
 }
 
+// Rows per workgroup of the small-tile GEMM (64 or 32) when the 128 x 128 GEMM would
+// not fill the chip well, else 0.  The 128 x 128 tiles fill the chip only from about
+// 1.5 tiles per CU; below that the 64 x 64 kernel runs four times as many workgroups
+// and is up to 2x faster (K=4096: N=14336 up to M=384, N=4096 up to M=1024).  Above it
+// the 128 x 128 kernel also needs its rounds (two workgroups per CU) well filled: 80%
+// over one or two rounds, 70% over more.  N=11008, M=768 is 516 tiles, a second round
+// for 4 of them (156 us against 128 us for the 64 x 64 kernel); 896 tiles (N=14336,
+// M=1024, 88%) stay on it (198 against 213 us), and so do 1120 (M=1280, three rounds 73%
+// full: 238 against 258 us).  Down to 1.5 workgroups of 64 x 64 per CU, 32-row tiles
+// (twice the workgroups, each wave half of a stage's blocks) are 7-20% faster still.
+int small_tile_rows(int N, int M) {
+    const int64_t cus = device_cus();
+    const int64_t t128 = (int64_t)((N + 127) / 128) * ((M + 127) / 128);
+    const int64_t slots = 2 * cus, rounds = (t128 + slots - 1) / slots;
+    const bool under = 2 * t128 < 3 * cus ||
+                       (rounds <= 2 ? 5 * t128 < 4 * slots * rounds : 10 * t128 < 7 * slots * rounds);
+    if (!under) return 0;
+    return 2 * (int64_t)((N + 63) / 64) * ((M + 63) / 64) <= 3 * cus ? 32 : 64;
+}
+
 int run_mm(const void *w, const void *xq, float *y, int K, int N, int M, int algo, hipStream_t s) {
     if (algo == JJO_ALGO_AUTO) {
         const bool gemv_ok = M <= kGemvMaxBatch && K <= kGemvMaxK && (int64_t)M * (K / 64) * 80 <= 150 * 1024;
@@ -174,22 +194,8 @@ int run_mm(const void *w, const void *xq, float *y, int K, int N, int M, int alg
             algo = JJO_ALGO_SKINNY;
         else if (gemv_ok)
             algo = JJO_ALGO_GEMV;
-        // The 128 x 128 tiles fill the chip only from about 1.5 tiles per CU; below
-        // that the 64 x 64 kernel runs four times as many workgroups and is up to 2x
-        // faster (K=4096: N=14336 up to M=384, N=4096 up to M=1024).  Above it the
-        // 128 x 128 kernel also needs its rounds (two workgroups per CU) well filled:
-        // 80% over one or two rounds, 70% over more.  N=11008, M=768 is 516 tiles, a
-        // second round for 4 of them (156 us against 128 us for the 64 x 64 kernel);
-        // 896 tiles (N=14336, M=1024, 88%) stay on it (198 against 213 us), and so do
-        // 1120 (M=1280, three rounds 73% full: 238 against 258 us).
-        else if (const int64_t t128 = (int64_t)((N + 127) / 128) * ((M + 127) / 128),
-                 slots = 2 * (int64_t)device_cus(), rounds = (t128 + slots - 1) / slots;
-                 2 * t128 < 3 * (int64_t)device_cus() ||
-                 (rounds <= 2 ? 5 * t128 < 4 * slots * rounds : 10 * t128 < 7 * slots * rounds))
-            // Down to 1.5 workgroups of 64 x 64 per CU, 32-row tiles (twice the
-            // workgroups, each wave half of a stage's blocks) are 7-20% faster still.
-            algo = 2 * (int64_t)((N + 63) / 64) * ((M + 63) / 64) <= 3 * (int64_t)device_cus() ? JJO_ALGO_MFMA32
-                                                                                            : JJO_ALGO_MFMA64;
+        else if (const int tr = small_tile_rows(N, M); tr != 0)
+            algo = tr == 32 ? JJO_ALGO_MFMA32 : JJO_ALGO_MFMA64;
         else
             algo = JJO_ALGO_MFMA;
     }
@@ -415,21 +421,33 @@ namespace {
 // Split-layout matmul from Q8_1 blocks (shapes validated by the caller).
 int run_mm_split(const void *w, const void *xq, float *y, int K, int N, int M, hipStream_t s) {
     const bool gemv_ok = M <= kGemvMaxBatch && K <= kGemvMaxK && (int64_t)M * (K / kQK) * 48 <= 150 * 1024;
-    // The crossovers of the block_q4_0 AUTO dispatch: the GEMV up to batch 4 (one
-    // K slice) or 2, the LDS-resident skinny kernel for 5..16, the GEMM above.
+    // The block_q4_0 AUTO dispatch's choices, each kernel reading the split layout: the
+    // GEMV up to batch 4 (one K slice) or 2, the LDS-resident skinny kernel for 5..16 at
+    // K <= 4096, the per-wave skinny kernel up to 32, then the small-tile GEMM while the
+    // 128 x 128 tiles would not fill the chip well, else the 128 x 128 GEMM.
+    hipError_t e;
     if (gemv_ok && M <= (K <= 4096 ? kGemvPreferredBatch : 2)) {
-        hipError_t e = launch_gemv_q4s(w, xq, y, K, N, M, s);
+        e = launch_gemv_q4s(w, xq, y, K, N, M, s);
         return e == hipSuccess ? JJO_OK : hip_fail(e, "gemv_q4s launch");
     }
-    if (M <= 16 && gemm_skinny_persist_supported(w, xq, K, M)) {
-        hipError_t e = launch_gemm_skinny_persist_layout(w, xq, y, K, N, M, true, s);
+    if (K <= 4096 && M >= 5 && M <= 16 && gemm_skinny_persist_supported(w, xq, K, M)) {
+        e = launch_gemm_skinny_persist_layout(w, xq, y, K, N, M, true, s);
         return e == hipSuccess ? JJO_OK : hip_fail(e, "gemm_skinny_persist (split layout) launch");
     }
+    if (gemm_skinny_supported(w, xq, K, M)) {
+        e = launch_gemm_skinny_layout(w, xq, y, K, N, M, true, s);
+        return e == hipSuccess ? JJO_OK : hip_fail(e, "gemm_skinny (split layout) launch");
+    }
     if (gemv_ok) {
-        hipError_t e = launch_gemv_q4s(w, xq, y, K, N, M, s);
+        e = launch_gemv_q4s(w, xq, y, K, N, M, s);
         return e == hipSuccess ? JJO_OK : hip_fail(e, "gemv_q4s launch");
     }
-    hipError_t e = launch_gemm_q4s_mfma(w, xq, y, K, N, M, true, s);
+    // K=14336, N=4096, M=48 on the 128 x 128 split GEMM: 126 us (32 workgroups).
+    if (const int tr = small_tile_rows(N, M); tr != 0) {
+        e = launch_gemm_mfma64(w, xq, y, K, N, M, s, tr, true);
+        return e == hipSuccess ? JJO_OK : hip_fail(e, "gemm_mfma64 (split layout) launch");
+    }
+    e = launch_gemm_q4s_mfma(w, xq, y, K, N, M, true, s);
     return e == hipSuccess ? JJO_OK : hip_fail(e, "gemm_q4s_mfma launch");
 }
 

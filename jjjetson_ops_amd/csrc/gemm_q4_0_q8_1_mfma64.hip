@@ -48,7 +48,10 @@ struct SmallTile {
     static constexpr int KS = TR == 64 ? 1 : 2;
 };
 
-template <int TR>
+// kSplit: the weights are in the split layout (a nibble plane, then an fp16 scale
+// plane); a thread's block is then one aligned 16-byte nibble load and one 2-byte
+// scale load, the same two vector-memory instructions.
+template <int TR, bool kSplit = false>
 __global__ __launch_bounds__(kSThreads) void gemm_q4_0_q8_1_mfma64_kernel(const uint8_t *__restrict__ w,
                                                                          const uint8_t *__restrict__ xq,
                                                                          float *__restrict__ y, int K, int N,
@@ -88,21 +91,38 @@ __global__ __launch_bounds__(kSThreads) void gemm_q4_0_q8_1_mfma64_kernel(const 
     const bool st_odd = st_blk & 1;
     const uint8_t *w_src =
         w + (size_t)min(n0 + st_row, N - 1) * row_bytes + (size_t)((st_blk * kQ4BlockBytes) & ~3);
+    // Split layout: block (row, st_blk) of stage 0 in the nibble and scale planes.
+    const int nb = K / kQK;
+    const size_t sblk = (size_t)min(n0 + st_row, N - 1) * nb + st_blk;
+    const uint8_t *wq_s = w + sblk * 16;
+    const uint16_t *wd_s = reinterpret_cast<const uint16_t *>(w + (size_t)N * nb * 16) + sblk;
     uint32_t wr0[5], wr1[5];
     // Two vector-memory instructions per call (the explicit waits count on it).
     auto load_w = [&](int c, uint32_t(&wst)[5]) {
-        const uint8_t *p = w_src + (size_t)c * (SKB * kQ4BlockBytes);
-        const u32x4a4 a = *reinterpret_cast<const u32x4a4 *>(p);
-        wst[0] = a.x; wst[1] = a.y; wst[2] = a.z; wst[3] = a.w;
-        wst[4] = *reinterpret_cast<const uint32_t *>(p + 16);
+        if constexpr (kSplit) {  // wst[0..3] the block's nibbles, wst[4] its scale
+            const u32x4 a = *reinterpret_cast<const u32x4 *>(wq_s + (size_t)c * (SKB * 16));
+            wst[0] = a.x; wst[1] = a.y; wst[2] = a.z; wst[3] = a.w;
+            wst[4] = wd_s[(size_t)c * SKB];
+        } else {
+            const uint8_t *p = w_src + (size_t)c * (SKB * kQ4BlockBytes);
+            const u32x4a4 a = *reinterpret_cast<const u32x4a4 *>(p);
+            wst[0] = a.x; wst[1] = a.y; wst[2] = a.z; wst[3] = a.w;
+            wst[4] = *reinterpret_cast<const uint32_t *>(p + 16);
+        }
     };
     auto store_w = [&](int buf, const uint32_t(&wst)[5]) {
         if (!st_store) return;
         uint8_t *wq = smem + kSOffW + buf * kSWBufBytes;
-        uint32_t q[4];
+        uint32_t q[4], dbits;
+        if constexpr (kSplit) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) q[k] = st_odd ? wst[k + 1] : __builtin_amdgcn_alignbyte(wst[k + 1], wst[k], 2);
-        const uint32_t dbits = st_odd ? (wst[0] >> 16) : (wst[0] & 0xffffu);
+            for (int k = 0; k < 4; ++k) q[k] = wst[k];
+            dbits = wst[4] & 0xffffu;
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) q[k] = st_odd ? wst[k + 1] : __builtin_amdgcn_alignbyte(wst[k + 1], wst[k], 2);
+            dbits = st_odd ? (wst[0] >> 16) : (wst[0] & 0xffffu);
+        }
         u32x4 lo, hi;
         lo.x = q[0] & 0x0f0f0f0fu; lo.y = q[1] & 0x0f0f0f0fu;
         lo.z = q[2] & 0x0f0f0f0fu; lo.w = q[3] & 0x0f0f0f0fu;
@@ -279,23 +299,26 @@ __global__ __launch_bounds__(kSThreads) void gemm_q4_0_q8_1_mfma64_kernel(const 
     }
 }
 
-template <int TR>
+template <int TR, bool kSplit>
 hipError_t launch_small(const void *w, const void *xq, float *y, int K, int N, int M, hipStream_t stream) {
     constexpr int smem = SmallTile<TR>::kSmemBytes;
-    hipError_t e = ensure_dynamic_lds((const void *)gemm_q4_0_q8_1_mfma64_kernel<TR>, smem);
+    hipError_t e = ensure_dynamic_lds((const void *)gemm_q4_0_q8_1_mfma64_kernel<TR, kSplit>, smem);
     if (e != hipSuccess) return e;
     const dim3 grid((N + TR - 1) / TR, (M + SBM - 1) / SBM);
-    hipLaunchKernelGGL(gemm_q4_0_q8_1_mfma64_kernel<TR>, grid, dim3(kSThreads), smem, stream, (const uint8_t *)w,
-                       (const uint8_t *)xq, y, K, N, M);
+    hipLaunchKernelGGL((gemm_q4_0_q8_1_mfma64_kernel<TR, kSplit>), grid, dim3(kSThreads), smem, stream,
+                       (const uint8_t *)w, (const uint8_t *)xq, y, K, N, M);
     return hipGetLastError();
 }
 
 }  // namespace
 
 hipError_t launch_gemm_mfma64(const void *w, const void *xq, float *y, int K, int N, int M, hipStream_t stream,
-                              int tile_rows) {
-    return tile_rows == 32 ? launch_small<32>(w, xq, y, K, N, M, stream)
-                           : launch_small<64>(w, xq, y, K, N, M, stream);
+                              int tile_rows, bool split) {
+    if (split)
+        return tile_rows == 32 ? launch_small<32, true>(w, xq, y, K, N, M, stream)
+                               : launch_small<64, true>(w, xq, y, K, N, M, stream);
+    return tile_rows == 32 ? launch_small<32, false>(w, xq, y, K, N, M, stream)
+                           : launch_small<64, false>(w, xq, y, K, N, M, stream);
 }
 
 }  // namespace jjo

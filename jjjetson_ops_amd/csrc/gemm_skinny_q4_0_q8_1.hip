@@ -37,6 +37,12 @@
 //     stage's 8 blocks into the same accumulator (fp16 x fp16 products are exact
 //     in fp32).  y = 8*acc.
 //
+// SPLIT: weights in the split layout (nibble plane + fp16 scale plane).  A stage of
+// RT*16 rows is then RT*16 x 128 nibble bytes (block j of row r in slot j ^ (r & 7) of
+// the row, against LDS bank conflicts) followed by the rows' 16-byte runs of 8 scales:
+// the same RT*2304 bytes and the same 2*RT + 1 DMA instructions (RT = 1, 2), with
+// aligned operand reads.
+//
 // Requirements (checked by the launcher): K % 256 == 0, w and xq 16-byte aligned.
 #include <hip/hip_fp16.h>
 
@@ -92,7 +98,7 @@ struct Lds {
 };
 
 
-template <int RT, int CT, int P, int KW>
+template <int RT, int CT, int P, int KW, bool SPLIT = false>
 __global__ __launch_bounds__(64 * KW) void gemm_skinny_kernel(const uint8_t *__restrict__ w,
                                                                   const uint8_t *__restrict__ xq,
                                                                   float *__restrict__ y, int K, int N, int M) {
@@ -128,6 +134,20 @@ __global__ __launch_bounds__(64 * KW) void gemm_skinny_kernel(const uint8_t *__r
         w_off[i] = (uint32_t)((size_t)(row - n0) * row_bytes) + 16u * piece;
     }
     const uint8_t *w_base = w + (size_t)n0 * row_bytes;
+    // Split layout: nibble chunk c = 64*i + lane -> row c / 8 of the tile, slot c % 8
+    // holding block (c % 8) ^ (row & 7) of the stage; scale run of row `lane` (< RT*16).
+    static_assert(!SPLIT || 2 * RT + 1 == G::kWInstr, "split stages use the block layout's DMA count");
+    uint32_t ws_off[2 * RT];
+#pragma unroll
+    for (int i = 0; i < 2 * RT; ++i) {
+        const int c = 64 * i + lane, rr = c >> 3;
+        const int row = min(n0 + rr, N - 1);
+        ws_off[i] = (uint32_t)((size_t)(row - n0) * nb * 16) + 16u * (uint32_t)((c & 7) ^ (rr & 7));
+    }
+    const uint8_t *ws_base = w + (size_t)n0 * nb * 16;
+    const uint8_t *wd_base = w + (size_t)N * nb * 16 + (size_t)n0 * nb * 2;
+    const uint32_t wd_off = (uint32_t)((size_t)(min(n0 + lane, N - 1) - n0) * nb * 2);
+    constexpr int kSplitNibBytes = RT * 16 * 128;  // scales follow the nibbles in a stage
     // activation: the stage's 288*M contiguous bytes
     const int x_run = 2 * kQ8BlockBytes * M;
     const int x_chunks = x_run / 16;
@@ -137,11 +157,22 @@ __global__ __launch_bounds__(64 * KW) void gemm_skinny_kernel(const uint8_t *__r
     auto issue = [&](int s) {  // stage s of this wave's slice into slot s % P
         uint8_t *st = ring + (s % P) * G::kStageBytes;
         const int gs = wave + KW * s;
+        if constexpr (SPLIT) {
+            const size_t blk0 = (size_t)gs * kStageBlocks;
+#pragma unroll
+            for (int i = 0; i < 2 * RT; ++i)
+                __builtin_amdgcn_global_load_lds((const void *)(ws_base + blk0 * 16 + ws_off[i]),
+                                                 (lds_void *)(st + 1024 * i), 16, 0, 0);
+            if (lane < RT * 16)
+                __builtin_amdgcn_global_load_lds((const void *)(wd_base + blk0 * 2 + wd_off),
+                                                 (lds_void *)(st + kSplitNibBytes), 16, 0, 0);
+        } else {
         const uint8_t *ws = w_base + (size_t)gs * kStageRowBytes;
 #pragma unroll
         for (int i = 0; i < G::kWInstr; ++i) {
             if (64 * i + lane < G::kWChunks || (G::kWChunks % 64) == 0)
                 __builtin_amdgcn_global_load_lds((const void *)(ws + w_off[i]), (lds_void *)(st + 1024 * i), 16, 0, 0);
+        }
         }
         const uint8_t *xs = xq + (size_t)gs * x_run;
         uint8_t *xd = st + G::kWBytes;
@@ -206,11 +237,15 @@ __global__ __launch_bounds__(64 * KW) void gemm_skinny_kernel(const uint8_t *__r
         // d_w of blocks 4(g&1)..4(g&1)+3 of this lane's weight row: the B operand of the s_x MFMA
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
-            const _Float16 *dr = reinterpret_cast<const _Float16 *>(st + (rt * 16 + l16) * kStageRowBytes +
-                                                                    (g & 1) * 4 * kQ4BlockBytes);
             f16x4 dw_op;
+            if constexpr (SPLIT) {
+                dw_op = *reinterpret_cast<const f16x4 *>(st + kSplitNibBytes + (rt * 16 + l16) * 16 + 8 * (g & 1));
+            } else {
+                const _Float16 *dr = reinterpret_cast<const _Float16 *>(st + (rt * 16 + l16) * kStageRowBytes +
+                                                                        (g & 1) * 4 * kQ4BlockBytes);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) dw_op[j] = dr[j * kQ4BlockBytes / 2];
+                for (int j = 0; j < 4; ++j) dw_op[j] = dr[j * kQ4BlockBytes / 2];
+            }
 #pragma unroll
             for (int ct = 0; ct < CT; ++ct)
                 acc[rt][ct] = __builtin_amdgcn_mfma_f32_16x16x16f16(sx_op[ct], dw_op, acc[rt][ct], 0, 0, 0);
@@ -232,15 +267,21 @@ __global__ __launch_bounds__(64 * KW) void gemm_skinny_kernel(const uint8_t *__r
             }
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) {
-                const uint8_t *wr = st + (rt * 16 + l16) * kStageRowBytes + bb * kQ4BlockBytes;
                 uint32_t q;
+                _Float16 dw;
+                if constexpr (SPLIT) {
+                    q = *reinterpret_cast<const uint32_t *>(st + (rt * 16 + l16) * 128 + (bb ^ (l16 & 7)) * 16 + 4 * g);
+                    dw = reinterpret_cast<const _Float16 *>(st + kSplitNibBytes + (rt * 16 + l16) * 16)[bb];
+                } else {
+                const uint8_t *wr = st + (rt * 16 + l16) * kStageRowBytes + bb * kQ4BlockBytes;
                 if ((bb & 1) == 0) {  // nibble dword g at 2 mod 4: re-align
                     const uint32_t *p = reinterpret_cast<const uint32_t *>(wr + 4 * g);
                     q = __builtin_amdgcn_alignbyte(p[1], p[0], 2);
                 } else {
                     q = *reinterpret_cast<const uint32_t *>(wr + 2 + 4 * g);
                 }
-                const _Float16 dw = *reinterpret_cast<const _Float16 *>(wr);
+                dw = *reinterpret_cast<const _Float16 *>(wr);
+                }
                 const long bop = (long)((uint64_t)((q >> 4) & 0x0f0f0f0fu) << 32 | (q & 0x0f0f0f0fu));
 #pragma unroll
                 for (int ct = 0; ct < CT; ++ct) {
@@ -301,10 +342,14 @@ __global__ __launch_bounds__(64 * KW) void gemm_skinny_kernel(const uint8_t *__r
 }
 
 template <int RT, int CT, int P, int KW>
-hipError_t launch_rcp(const void *w, const void *xq, float *y, int K, int N, int M, hipStream_t stream) {
+hipError_t launch_rcp(const void *w, const void *xq, float *y, int K, int N, int M, bool split, hipStream_t stream) {
     const int blocks = (N + 16 * RT - 1) / (16 * RT);
-    hipLaunchKernelGGL((gemm_skinny_kernel<RT, CT, P, KW>), dim3(blocks), dim3(64 * KW), 0, stream,
-                       (const uint8_t *)w, (const uint8_t *)xq, y, K, N, M);
+    if (split)
+        hipLaunchKernelGGL((gemm_skinny_kernel<RT, CT, P, KW, true>), dim3(blocks), dim3(64 * KW), 0, stream,
+                           (const uint8_t *)w, (const uint8_t *)xq, y, K, N, M);
+    else
+        hipLaunchKernelGGL((gemm_skinny_kernel<RT, CT, P, KW, false>), dim3(blocks), dim3(64 * KW), 0, stream,
+                           (const uint8_t *)w, (const uint8_t *)xq, y, K, N, M);
     return hipGetLastError();
 }
 
@@ -318,16 +363,21 @@ bool gemm_skinny_supported(const void *w, const void *xq, int K, int M) {
     return K % 256 == 0 && M >= 1 && M <= kSkinnyMaxBatch && ((uintptr_t)w & 15) == 0 && ((uintptr_t)xq & 15) == 0;
 }
 
-hipError_t launch_gemm_skinny(const void *w, const void *xq, float *y, int K, int N, int M, hipStream_t stream) {
+hipError_t launch_gemm_skinny_layout(const void *w, const void *xq, float *y, int K, int N, int M, bool split,
+                                     hipStream_t stream) {
     if (!gemm_skinny_supported(w, xq, K, M)) return hipErrorInvalidValue;
     if (M <= 16) {
         // 32-row workgroups of 4 K-slice waves while that fills the chip; for short
         // matrices (N < 8192) 16-row workgroups of 8 K-slice waves (twice the
         // workgroups, each CU holding one).
-        if ((N + 31) / 32 >= 256) return launch_rcp<kSkinnyRt, 1, kSkinnyP, 4>(w, xq, y, K, N, M, stream);
-        return launch_rcp<1, 1, kSkinnyP, 8>(w, xq, y, K, N, M, stream);
+        if ((N + 31) / 32 >= 256) return launch_rcp<kSkinnyRt, 1, kSkinnyP, 4>(w, xq, y, K, N, M, split, stream);
+        return launch_rcp<1, 1, kSkinnyP, 8>(w, xq, y, K, N, M, split, stream);
     }
-    return launch_rcp<kSkinnyRt, 2, kSkinnyP, 4>(w, xq, y, K, N, M, stream);
+    return launch_rcp<kSkinnyRt, 2, kSkinnyP, 4>(w, xq, y, K, N, M, split, stream);
+}
+
+hipError_t launch_gemm_skinny(const void *w, const void *xq, float *y, int K, int N, int M, hipStream_t stream) {
+    return launch_gemm_skinny_layout(w, xq, y, K, N, M, false, stream);
 }
 
 }  // namespace jjo

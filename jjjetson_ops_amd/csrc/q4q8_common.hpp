@@ -61,6 +61,9 @@ hipError_t launch_q4_0_to_split(const void *w, void *out, int64_t n_blocks, hipS
 bool gemm_skinny_supported(const void *w, const void *xq, int K, int M);
 hipError_t launch_gemm_skinny(const void *w, const void *xq, float *y, int K, int N, int M,
                               hipStream_t stream);
+// The same kernel on split-layout weights (split = true).
+hipError_t launch_gemm_skinny_layout(const void *w, const void *xq, float *y, int K, int N, int M, bool split,
+                                     hipStream_t stream);
 // Batch <= 16: activation resident in LDS, up to 4 weight tiles per workgroup.
 bool gemm_skinny_persist_supported(const void *w, const void *xq, int K, int M);
 hipError_t launch_gemm_skinny_persist(const void *w, const void *xq, float *y, int K, int N, int M,
@@ -69,8 +72,9 @@ hipError_t launch_gemm_skinny_persist(const void *w, const void *xq, float *y, i
 hipError_t launch_gemm_skinny_persist_layout(const void *w, const void *xq, float *y, int K, int N, int M, bool split,
                                              hipStream_t stream);
 // tile_rows: 64, or 32 (the stage's blocks split between wave pairs).
+// split: the weights are in the split layout (16-byte aligned).
 hipError_t launch_gemm_mfma64(const void *w, const void *xq, float *y, int K, int N, int M,
-                              hipStream_t stream, int tile_rows);
+                              hipStream_t stream, int tile_rows, bool split = false);
 hipError_t launch_gemm_mfma(const void *w, const void *xq, float *y, int K, int N, int M,
                             hipStream_t stream);
 hipError_t launch_gemm_mfma_grouped(const void *w, const void *xq, const int32_t *expert_offsets,

@@ -131,7 +131,11 @@ def test_split_f32_batch(M, dev):
                                    (11264, 77, 12), (256, 33, 16), (4096, 14336, 16), (4096, 70, 17),
                                    # K % 256 != 0: the skinny kernel is unsupported, batch 3/6 take
                                    # the GEMV (two K slices), batch 12 the GEMM
-                                   (4224, 100, 3), (4224, 100, 6), (4224, 100, 12)])
+                                   (4224, 100, 3), (4224, 100, 6), (4224, 100, 12),
+                                   # the per-wave skinny kernel (batch 17..32; 3..16 above K = 4096)
+                                   (4096, 300, 24), (4096, 1000, 32), (11008, 257, 3), (14336, 200, 9),
+                                   # the small-tile GEMM, 32- and 64-row tiles
+                                   (4096, 4096, 48), (4096, 1000, 64), (14336, 520, 200)])
 def test_split_gemm(K, N, M, dev):
     import torch
     note(f"split gemm M={M} K={K} N={N}")
