@@ -789,8 +789,20 @@ struct MoeWs {
     int32_t *ids, *offsets, *src_route, *dst_of_route;
     uint8_t *xq, *xp, *midq;
     float *eout;
+    float *gate_up;  // [R][2I] fp32, decode path only
     int64_t bytes;
 };
+
+// Token counts up to which the FFN runs its expert matrices as routed GEMVs (one
+// workgroup row range per active expert, every weight byte of an active expert
+// read once per chunk of its routes) instead of 128-row MFMA tiles, which leave
+// most of the GPU idle when each expert holds a handful of routes.
+#ifndef JJO_MOE_GEMV_TOKENS
+#define JJO_MOE_GEMV_TOKENS 12
+#endif
+bool moe_decode_path(int T, int H, int I, int top_k) {
+    return T <= JJO_MOE_GEMV_TOKENS && T * top_k <= kMoeDecodeRoutes && H <= 16384 && I <= 16384;
+}
 
 // Workspace carve-up, every part 256-byte aligned.
 MoeWs moe_ws_layout(uint8_t *base, int T, int H, int I, int E, int top_k) {
@@ -811,6 +823,7 @@ MoeWs moe_ws_layout(uint8_t *base, int T, int H, int I, int E, int top_k) {
     w.xp = take(R * (H / kQSuper) * kQ8BlockBytes);
     w.midq = take(R * (I / kQSuper) * kQ8BlockBytes);
     w.eout = (float *)take(R * H * 4);
+    w.gate_up = moe_decode_path(T, H, I, top_k) ? (float *)take(R * 2 * I * 4) : nullptr;
     w.bytes = off;
     return w;
 }
@@ -955,6 +968,26 @@ int moe_ffn_run(bool split, void *stream, const float *x, const float *logits, c
     hipStream_t s = (hipStream_t)stream;
     const int R = T * top_k;
     hipError_t e;
+    if (moe_decode_path(T, H, I, top_k)) {
+        // A token's top_k experts are distinct: no expert holds more than T routes.
+        // 1) quantize + top-k + dispatch + gather, 2) gate|up (both matrices, one
+        // launch) -> fp32 [R][2I], 3) SwiGLU + Q8_1, 4) down projection, 5) combine
+        if ((e = launch_moe_route_decode(x, logits, T, H, E, top_k, ws.route_w, ws.ids, ws.offsets, ws.src_route,
+                                         ws.dst_of_route, ws.xp, s)) != hipSuccess)
+            return hip_fail(e, "moe_ffn routing");
+        const int per_expert = T < R ? T : R;
+        if ((e = launch_gemv_routed(w_gate, w_up, ws.xp, ws.offsets, E, R, per_expert, ws.gate_up, 2 * I, H, I,
+                                    split, s)) != hipSuccess)
+            return hip_fail(e, "moe_ffn gate_up (routed GEMV)");
+        if ((e = launch_swiglu_quantize_q8_1(ws.gate_up, ws.midq, nullptr, I, R, s)) != hipSuccess)
+            return hip_fail(e, "moe_ffn swiglu");
+        if ((e = launch_gemv_routed(w_down, nullptr, ws.midq, ws.offsets, E, R, per_expert, ws.eout, H, I, H, split,
+                                    s)) != hipSuccess)
+            return hip_fail(e, "moe_ffn down (routed GEMV)");
+        if ((e = launch_moe_combine(ws.eout, ws.dst_of_route, ws.route_w, y, T, H, top_k, s)) != hipSuccess)
+            return hip_fail(e, "moe_ffn combine");
+        return JJO_OK;
+    }
     // 1) x -> Q8_1 (once per token), 2) top-k gating, 3) stable dispatch + Q8_1 row gather
     if ((e = launch_quantize_q8_1(x, ws.xq, H, T, 1, s)) != hipSuccess) return hip_fail(e, "moe_ffn quantize x");
     if ((e = launch_moe_top_k(logits, ws.route_w, ws.ids, T, E, top_k, s)) != hipSuccess)

@@ -282,14 +282,94 @@ __device__ __forceinline__ void finish_f32(uint8_t *xs, uint8_t *__restrict__ xq
     }
 }
 
+// ---- routed (MoE decode) launches ----
+// The weights are E stacked [N][K] expert matrices and the activation is the
+// expert-sorted Q8_1 route rows (superblock-major over n_routes rows); routes
+// offsets[e]..offsets[e+1]-1 use expert e.  blockIdx.y = which * slots + slot
+// selects the slot-th expert that has routes (which = 1: the second stacked
+// matrix w2, written N columns further along each output row), blockIdx.z the
+// chunk of M of its routes.  Output row p (a sorted route position) starts at
+// y + p * ldy.
+struct RouteArgs {
+    const int32_t *offsets;  // [n_experts + 1]
+    const uint8_t *w2;       // second stacked matrix, or null
+    int n_experts, n_routes, slots, ldy;
+};
+
+struct RouteTile {
+    int expert, which, m0, mc;  // routes m0 .. m0 + mc - 1 of `expert`
+};
+
+// Clamped route range of expert e (a malformed table gives fewer routes, never
+// an access outside the activation or output rows).
+__device__ __forceinline__ void expert_range(const RouteArgs &ra, int e, int &beg, int &end) {
+    beg = min(max(ra.offsets[e], 0), ra.n_routes);
+    end = min(max(ra.offsets[e + 1], beg), ra.n_routes);
+}
+
+// false: this workgroup has no routes (the same for all its waves).
+__device__ __forceinline__ bool route_tile(const RouteArgs &ra, int mt, RouteTile &t) {
+    const int which = (int)blockIdx.y >= ra.slots;
+    int slot = (int)blockIdx.y - which * ra.slots;
+    const int lane = threadIdx.x & 63;
+    int e = -1;
+    for (int e0 = 0; e0 < ra.n_experts; e0 += 64) {
+        bool nonempty = false;
+        if (e0 + lane < ra.n_experts) {
+            int b, en;
+            expert_range(ra, e0 + lane, b, en);
+            nonempty = en > b;
+        }
+        uint64_t bal = __ballot(nonempty);
+        const int c = __popcll(bal);
+        if (slot < c) {
+            for (int i = 0; i < slot; ++i) bal &= bal - 1;
+            e = e0 + __builtin_ctzll(bal);
+            break;
+        }
+        slot -= c;
+    }
+    if (e < 0) return false;
+    int beg, end;
+    expert_range(ra, e, beg, end);
+    const int m0 = beg + (int)blockIdx.z * mt;
+    if (m0 >= end) return false;
+    t.expert = e;
+    t.which = which;
+    t.m0 = m0;
+    t.mc = min(mt, end - m0);
+    return true;
+}
+
+// issue_q8 for routed launches: token m of the chunk reads route row
+// m0 + min(m, mc - 1) of the n_routes-row activation (tokens past the chunk's
+// routes re-read its last one; their sums are never stored).
+template <int M>
+__device__ __forceinline__ void issue_q8_routed(ItemQ8 &it, const uint8_t *__restrict__ xq, int item, int nb,
+                                                int n_routes, int m0, int mc) {
+    item = min(item, M * nb - 1);
+    const int m = item / nb, b = item - m * nb;
+    const int row = m0 + min(m, mc - 1);
+    const uint8_t *blk = xq + ((size_t)(b >> 2) * n_routes + row) * kQ8BlockBytes;
+    const int g = b & 3;
+    it.ds = *reinterpret_cast<const uint32_t *>(blk + 4 * g);
+    const u32x4a16 v0 = *reinterpret_cast<const u32x4a16 *>(blk + 16 + 32 * g);
+    const u32x4a16 v1 = *reinterpret_cast<const u32x4a16 *>(blk + 32 + 32 * g);
+    it.q[0] = v0.x; it.q[1] = v0.y; it.q[2] = v0.z; it.q[3] = v0.w;
+    it.q[4] = v1.x; it.q[5] = v1.y; it.q[6] = v1.z; it.q[7] = v1.w;
+}
+
 // Workgroup = RG row groups x JS K-slices (one wave each).  JS = ceil(K / 4096).
 // FUSED: `xin` is the fp32 activation [K] (M = 1) instead of Q8_1 blocks and
 // `xq_out` (optional) receives its Q8_1 bytes (written by workgroup 0).
-template <int M, int U, int JS, int RG, bool FUSED, int EARLY>
+// ROUTED: a routed launch (RouteArgs), M routes per workgroup, Q8_1 input.
+template <int M, int U, int JS, int RG, bool FUSED, int EARLY, bool ROUTED = false>
 __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint8_t *__restrict__ w,
                                                                       const void *__restrict__ xin,
                                                                       uint8_t *__restrict__ xq_out,
-                                                                      float *__restrict__ y, int K, int N) {
+                                                                      float *__restrict__ y, int K, int N,
+                                                                      RouteArgs ra) {
+    static_assert(!(ROUTED && FUSED), "routed launches take Q8_1 route rows");
     extern __shared__ __align__(16) uint8_t xs[];  // M * K/64 records of kRec bytes + 1 spare
     __shared__ float part[JS > 1 ? RG * JS * U * M : 1];
 
@@ -306,6 +386,13 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
     const int r0 = (blockIdx.x * RG + rg) * U;
     const int n_items = FUSED ? 2 * nb : M * nb;
     const int rounds = (n_items + kThreadsWG - 1) / kThreadsWG;
+    RouteTile rt{0, 0, 0, M};
+    if constexpr (ROUTED) {
+        if (!route_tile(ra, M, rt)) return;
+        w = (rt.which ? ra.w2 : w) + (size_t)rt.expert * N * row_bytes;
+        y += (size_t)rt.m0 * ra.ldy + (size_t)rt.which * N;
+    }
+    const int ldy = ROUTED ? ra.ldy : N;
 
     // All global loads below are unconditional (clamped addresses), so the
     // compiler can count them and wait for exactly the ones each step needs.
@@ -318,7 +405,10 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
         if constexpr (FUSED) {
             issue_f32(early[r], reinterpret_cast<const float *>(xin), item, nb);
         } else {
-            issue_q8<M>(early[r], reinterpret_cast<const uint8_t *>(xin), item, nb);
+            if constexpr (ROUTED)
+                issue_q8_routed<M>(early[r], reinterpret_cast<const uint8_t *>(xin), item, nb, ra.n_routes, rt.m0, rt.mc);
+            else
+                issue_q8<M>(early[r], reinterpret_cast<const uint8_t *>(xin), item, nb);
         }
     }
     // Keep the instruction scheduler from hoisting the weight loads above them.
@@ -352,7 +442,10 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
             issue_f32(it, reinterpret_cast<const float *>(xin), item, nb);
             finish_f32(xs, xq_w, it, item, nb, item < n_items);
         } else {
-            issue_q8<M>(it, reinterpret_cast<const uint8_t *>(xin), item, nb);
+            if constexpr (ROUTED)
+                issue_q8_routed<M>(it, reinterpret_cast<const uint8_t *>(xin), item, nb, ra.n_routes, rt.m0, rt.mc);
+            else
+                issue_q8<M>(it, reinterpret_cast<const uint8_t *>(xin), item, nb);
             finish_q8(xs, it, item, nb, n_items);
         }
     }
@@ -365,7 +458,47 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
 #pragma unroll
         for (int m = 0; m < M; ++m) acc[u][m] = 0.0f;
 
-    if (live) {
+    if (ROUTED && live) {
+        // Token-outer: tokens past this expert's routes (mc <= M, uniform over the
+        // workgroup) cost no dot products; each (row, token) sum is the same
+        // expression as below.
+        uint32_t qa[U][4], qb[U][4];
+        int32_t na[U], nbs[U];
+        float dwa[U], dwb[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                qa[u][i] = __builtin_amdgcn_alignbyte(wb[u].d[i + 1], wb[u].d[i], 2);
+                qb[u][i] = wb[u].d[i + 5];
+            }
+            na[u] = nib_sum128(qa[u]);
+            nbs[u] = nib_sum128(qb[u]);
+            dwa[u] = half_lo(wb[u].d[0]);
+            dwb[u] = half_hi(wb[u].d[4]);
+        }
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            if (m < rt.mc) {
+                const uint8_t *rec = xs + ((size_t)m * P + p) * kRec;
+                const u32x4a16 ha = *reinterpret_cast<const u32x4a16 *>(rec);
+                const u32x4a16 la = *reinterpret_cast<const u32x4a16 *>(rec + 16);
+                const u32x4a16 hb = *reinterpret_cast<const u32x4a16 *>(rec + 32);
+                const u32x4a16 lb = *reinterpret_cast<const u32x4a16 *>(rec + 48);
+                const f32x4 cst = *reinterpret_cast<const f32x4 *>(rec + 64);
+                const uint32_t hia[4] = {ha.x, ha.y, ha.z, ha.w}, loa[4] = {la.x, la.y, la.z, la.w};
+                const uint32_t hib[4] = {hb.x, hb.y, hb.z, hb.w}, lob[4] = {lb.x, lb.y, lb.z, lb.w};
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int32_t sa = block_sumi(qa[u], hia, loa, na[u]);
+                    const int32_t sb = block_sumi(qb[u], hib, lob, nbs[u]);
+                    float a = dwa[u] * fmaf((float)sa, cst.x, cst.y);
+                    a = fmaf(dwb[u], fmaf((float)sb, cst.z, cst.w), a);
+                    acc[u][m] = a;
+                }
+            }
+        }
+    } else if (live) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             uint32_t qa[4], qb[4];
@@ -407,7 +540,7 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
     const int u = idx / M, m = idx % M;
     const bool owner = (lane & (64 / NV - 1)) == 0 && idx < U * M;
     if constexpr (JS == 1) {
-        if (owner && r0 + u < N) y[(size_t)m * N + r0 + u] = s;
+        if (owner && r0 + u < N) if (m < rt.mc) y[(size_t)m * ldy + r0 + u] = s;
     } else {
         if (owner) part[((rg * U + u) * M + m) * JS + js] = s;
         __syncthreads();
@@ -421,7 +554,7 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
                         float s = pp[0];
 #pragma unroll
                         for (int j = 1; j < JS; ++j) s += pp[j];
-                        y[(size_t)m * N + r0 + u] = s;
+                        if (m < rt.mc) y[(size_t)m * ldy + r0 + u] = s;
                     }
                 }
         }
@@ -516,11 +649,15 @@ __device__ __forceinline__ void finish_f32_s(uint8_t *xs, uint8_t *__restrict__ 
 // 128*js + 64 + l of its wave's U rows.  Each of those blocks is one nontemporal
 // 16-byte load (plus a 2-byte scale load); the integer dot is the dot8 plane form
 // of gemv_q4_0_q8_1_kernel.
-template <int M, int U, int JS, int RG, bool FUSED, int EARLY>
+// ROUTED: a routed launch (RouteArgs) over E stacked split-layout experts (one
+// nibble plane over all E * N rows, then one scale plane), Q8_1 input.
+template <int M, int U, int JS, int RG, bool FUSED, int EARLY, bool ROUTED = false>
 __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *__restrict__ w,
                                                                 const void *__restrict__ xin,
                                                                 uint8_t *__restrict__ xq_out,
-                                                                float *__restrict__ y, int K, int N) {
+                                                                float *__restrict__ y, int K, int N,
+                                                                RouteArgs ra) {
+    static_assert(!(ROUTED && FUSED), "routed launches take Q8_1 route rows");
     extern __shared__ __align__(16) uint8_t xs[];  // M * K/32 records of kRecS bytes + 1 spare
     __shared__ float part[JS > 1 ? RG * JS * U * M : 1];
 
@@ -533,10 +670,20 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
     const int bk0 = 128 * js + lane;       // this lane's two blocks
     const int bk1 = bk0 + 64;
     const int c0 = min(bk0, nb - 1), c1 = min(bk1, nb - 1);
-    const uint16_t *__restrict__ dpl = reinterpret_cast<const uint16_t *>(w + (size_t)N * nb * 16);
     const int r0 = (blockIdx.x * RG + rg) * U;
     const int n_items = FUSED ? 2 * nb : M * nb;
     const int rounds = (n_items + kThreadsWG - 1) / kThreadsWG;
+    RouteTile rt{0, 0, 0, M};
+    size_t plane_rows = N, row0 = 0;  // rows of the buffer's planes, first row of this matrix
+    if constexpr (ROUTED) {
+        if (!route_tile(ra, M, rt)) return;
+        if (rt.which) w = ra.w2;
+        plane_rows = (size_t)ra.n_experts * N;
+        row0 = (size_t)rt.expert * N;
+        y += (size_t)rt.m0 * ra.ldy + (size_t)rt.which * N;
+    }
+    const int ldy = ROUTED ? ra.ldy : N;
+    const uint16_t *__restrict__ dpl = reinterpret_cast<const uint16_t *>(w + plane_rows * nb * 16);
 
     // 1) activation requests (L2-resident), ahead of the weights
     using Item = typename std::conditional<FUSED, ItemF32, ItemQ8>::type;
@@ -547,7 +694,10 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
         if constexpr (FUSED) {
             issue_f32(early[r], reinterpret_cast<const float *>(xin), item, nb);
         } else {
-            issue_q8<M>(early[r], reinterpret_cast<const uint8_t *>(xin), item, nb);
+            if constexpr (ROUTED)
+                issue_q8_routed<M>(early[r], reinterpret_cast<const uint8_t *>(xin), item, nb, ra.n_routes, rt.m0, rt.mc);
+            else
+                issue_q8<M>(early[r], reinterpret_cast<const uint8_t *>(xin), item, nb);
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -556,7 +706,7 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
     uint32_t wd[U][2];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-        const size_t base = (size_t)min(r0 + u, N - 1) * nb;
+        const size_t base = (row0 + (size_t)min(r0 + u, N - 1)) * nb;
         wq[u][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4a16 *>(w + (base + c0) * 16));
         wq[u][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4a16 *>(w + (base + c1) * 16));
         wd[u][0] = dpl[base + c0];
@@ -581,7 +731,10 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
             issue_f32(it, reinterpret_cast<const float *>(xin), item, nb);
             finish_f32_s(xs, xq_w, it, item, nb, item < n_items);
         } else {
-            issue_q8<M>(it, reinterpret_cast<const uint8_t *>(xin), item, nb);
+            if constexpr (ROUTED)
+                issue_q8_routed<M>(it, reinterpret_cast<const uint8_t *>(xin), item, nb, ra.n_routes, rt.m0, rt.mc);
+            else
+                issue_q8<M>(it, reinterpret_cast<const uint8_t *>(xin), item, nb);
             finish_q8_s(xs, it, item, nb, n_items);
         }
     }
@@ -594,6 +747,41 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
 #pragma unroll
         for (int m = 0; m < M; ++m) acc[u][m] = 0.0f;
 
+    if constexpr (ROUTED) {
+        // Token-outer (as in gemv_q4_0_q8_1_kernel): tokens past the expert's routes
+        // cost no dot products; every sum adds block k = 0, then k = 1, as below.
+        int32_t ns[U][2];
+        float dw[U][2];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const uint32_t q[4] = {wq[u][k].x, wq[u][k].y, wq[u][k].z, wq[u][k].w};
+                ns[u][k] = nib_sum128(q);
+                dw[u][k] = __half2float(__ushort_as_half((unsigned short)wd[u][k]));
+            }
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            if (m < rt.mc) {
+#pragma unroll
+                for (int k = 0; k < 2; ++k) {
+                    const bool live = (k ? bk1 : bk0) < nb;
+                    const uint8_t *rec = xs + ((size_t)m * nb + (k ? c1 : c0)) * kRecS;
+                    const u32x4a16 h4 = *reinterpret_cast<const u32x4a16 *>(rec);
+                    const u32x4a16 l4 = *reinterpret_cast<const u32x4a16 *>(rec + 16);
+                    const u32x2a8 c2 = *reinterpret_cast<const u32x2a8 *>(rec + 32);
+                    const uint32_t hi[4] = {h4.x, h4.y, h4.z, h4.w}, lo[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        const uint32_t q[4] = {wq[u][k].x, wq[u][k].y, wq[u][k].z, wq[u][k].w};
+                        const int32_t sv = block_sumi(q, hi, lo, ns[u][k]);
+                        const float v = dw[u][k] * fmaf((float)sv, __uint_as_float(c2.x), __uint_as_float(c2.y));
+                        acc[u][m] += live ? v : 0.0f;
+                    }
+                }
+            }
+        }
+    } else {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
 #pragma unroll
@@ -616,6 +804,7 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
             }
         }
     }
+    }
 
     constexpr int NV = pow2_at_least(U * M);
     float v[NV];
@@ -626,7 +815,7 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
     const int u = idx / M, m = idx % M;
     const bool owner = (lane & (64 / NV - 1)) == 0 && idx < U * M;
     if constexpr (JS == 1) {
-        if (owner && r0 + u < N) y[(size_t)m * N + r0 + u] = s;
+        if (owner && r0 + u < N) if (m < rt.mc) y[(size_t)m * ldy + r0 + u] = s;
     } else {
         if (owner) part[((rg * U + u) * M + m) * JS + js] = s;
         __syncthreads();
@@ -640,7 +829,7 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
                         float s = pp[0];
 #pragma unroll
                         for (int j = 1; j < JS; ++j) s += pp[j];
-                        y[(size_t)m * N + r0 + u] = s;
+                        if (m < rt.mc) y[(size_t)m * ldy + r0 + u] = s;
                     }
                 }
         }
@@ -686,47 +875,73 @@ constexpr int rg_for_s() {
     return JS == 1 ? kRgM : JS == 2 ? 2 : 1;
 }
 
-template <bool SPLIT, int M, int U, int JS, bool FUSED, int EARLY>
-hipError_t launch_cfg(const void *w, const void *xin, uint8_t *xq_out, float *y, int K, int N, hipStream_t stream) {
-    constexpr int RG = SPLIT ? rg_for_s<M, JS, FUSED>() : rg_for<M, JS, FUSED>();
+// Routed launches: every workgroup stages its routes' whole activation rows, so
+// long rows (the down projection's K = I) want more row groups per workgroup to
+// spread that staging over more weight rows.
+#ifndef JJO_RT_RG2
+#define JJO_RT_RG2 4
+#endif
+#ifndef JJO_RT_RG3
+#define JJO_RT_RG3 4
+#endif
+#ifndef JJO_RT_RG4
+#define JJO_RT_RG4 4
+#endif
+template <bool SPLIT, int M, int JS, bool FUSED, bool ROUTED>
+constexpr int rg_pick() {
+    if (ROUTED && JS == 2) return JJO_RT_RG2;
+    if (ROUTED && JS == 3) return JJO_RT_RG3;
+    if (ROUTED && JS == 4) return JJO_RT_RG4;
+    return SPLIT ? rg_for_s<M, JS, FUSED>() : rg_for<M, JS, FUSED>();
+}
+
+// Routed launches (ROUTED) run gz token chunks over the gy expert slots of `ra`.
+template <bool SPLIT, int M, int U, int JS, bool FUSED, int EARLY, bool ROUTED = false>
+hipError_t launch_cfg(const void *w, const void *xin, uint8_t *xq_out, float *y, int K, int N, hipStream_t stream,
+                      const RouteArgs &ra = RouteArgs{}, int gy = 1, int gz = 1) {
+    constexpr int RG = rg_pick<SPLIT, M, JS, FUSED, ROUTED>();
     const int groups = (N + U - 1) / U;
     const int blocks = (groups + RG - 1) / RG;
     const size_t smem = SPLIT ? ((size_t)M * (K / 32) + 1) * kRecS : ((size_t)M * (K / 64) + 1) * kRec;
-    const void *kern = SPLIT ? (const void *)gemv_q4s_kernel<M, U, JS, RG, FUSED, EARLY>
-                             : (const void *)gemv_q4_0_q8_1_kernel<M, U, JS, RG, FUSED, EARLY>;
+    const void *kern = SPLIT ? (const void *)gemv_q4s_kernel<M, U, JS, RG, FUSED, EARLY, ROUTED>
+                             : (const void *)gemv_q4_0_q8_1_kernel<M, U, JS, RG, FUSED, EARLY, ROUTED>;
     if (smem > 64 * 1024) {
         // Raise this instantiation's dynamic-LDS limit to what the call needs.
         hipError_t e = ensure_dynamic_lds(kern, smem);
         if (e != hipSuccess) return e;
     }
     if constexpr (SPLIT) {
-        hipLaunchKernelGGL((gemv_q4s_kernel<M, U, JS, RG, FUSED, EARLY>), dim3(blocks), dim3(64 * JS * RG), smem,
-                           stream, (const uint8_t *)w, xin, xq_out, y, K, N);
+        hipLaunchKernelGGL((gemv_q4s_kernel<M, U, JS, RG, FUSED, EARLY, ROUTED>), dim3(blocks, gy, gz),
+                           dim3(64 * JS * RG), smem, stream, (const uint8_t *)w, xin, xq_out, y, K, N, ra);
     } else {
-        hipLaunchKernelGGL((gemv_q4_0_q8_1_kernel<M, U, JS, RG, FUSED, EARLY>), dim3(blocks), dim3(64 * JS * RG),
-                           smem, stream, (const uint8_t *)w, xin, xq_out, y, K, N);
+        hipLaunchKernelGGL((gemv_q4_0_q8_1_kernel<M, U, JS, RG, FUSED, EARLY, ROUTED>), dim3(blocks, gy, gz),
+                           dim3(64 * JS * RG), smem, stream, (const uint8_t *)w, xin, xq_out, y, K, N, ra);
     }
     return hipGetLastError();
 }
 
-template <bool SPLIT, int M, int U, int JS, bool FUSED>
-hipError_t launch_js(const void *w, const void *xin, uint8_t *xq_out, float *y, int K, int N, hipStream_t stream) {
-    constexpr int RG = SPLIT ? rg_for_s<M, JS, FUSED>() : rg_for<M, JS, FUSED>();
+template <bool SPLIT, int M, int U, int JS, bool FUSED, bool ROUTED = false>
+hipError_t launch_js(const void *w, const void *xin, uint8_t *xq_out, float *y, int K, int N, hipStream_t stream,
+                     const RouteArgs &ra = RouteArgs{}, int gy = 1, int gz = 1) {
+    constexpr int RG = rg_pick<SPLIT, M, JS, FUSED, ROUTED>();
     const int n_items = FUSED ? 2 * (K / kQK) : M * (K / kQK);
     const int rounds = (n_items + 64 * JS * RG - 1) / (64 * JS * RG);
-    if (rounds <= 1) return launch_cfg<SPLIT, M, U, JS, FUSED, 1>(w, xin, xq_out, y, K, N, stream);
-    if (rounds <= 2) return launch_cfg<SPLIT, M, U, JS, FUSED, 2>(w, xin, xq_out, y, K, N, stream);
-    return launch_cfg<SPLIT, M, U, JS, FUSED, 4>(w, xin, xq_out, y, K, N, stream);
+    if (rounds <= 1) return launch_cfg<SPLIT, M, U, JS, FUSED, 1, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy, gz);
+    if (rounds <= 2) return launch_cfg<SPLIT, M, U, JS, FUSED, 2, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy, gz);
+    return launch_cfg<SPLIT, M, U, JS, FUSED, 4, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy, gz);
 }
 
-template <bool SPLIT, int M, int U, bool FUSED>
-hipError_t launch_m(const void *w, const void *xin, uint8_t *xq_out, float *y, int K, int N, hipStream_t stream) {
+template <bool SPLIT, int M, int U, bool FUSED, bool ROUTED = false>
+hipError_t launch_m(const void *w, const void *xin, uint8_t *xq_out, float *y, int K, int N, hipStream_t stream,
+                    const RouteArgs &ra = RouteArgs{}, int gy = 1, int gz = 1) {
     const int js = (K / 64 + 63) / 64;
     switch (js) {
-        case 1: return launch_js<SPLIT, M, U, 1, FUSED>(w, xin, xq_out, y, K, N, stream);
-        case 2: return launch_js<SPLIT, M, U, 2, FUSED>(w, xin, xq_out, y, K, N, stream);
-        case 3: return launch_js<SPLIT, M, (SPLIT && M == 1 && !FUSED) ? 2 : U, 3, FUSED>(w, xin, xq_out, y, K, N, stream);
-        case 4: return launch_js<SPLIT, M, U, 4, FUSED>(w, xin, xq_out, y, K, N, stream);
+        case 1: return launch_js<SPLIT, M, U, 1, FUSED, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy, gz);
+        case 2: return launch_js<SPLIT, M, U, 2, FUSED, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy, gz);
+        case 3:
+            return launch_js<SPLIT, M, (SPLIT && M == 1 && !FUSED) ? 2 : U, 3, FUSED, ROUTED>(w, xin, xq_out, y, K, N,
+                                                                                           stream, ra, gy, gz);
+        case 4: return launch_js<SPLIT, M, U, 4, FUSED, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy, gz);
         default: return hipErrorInvalidValue;  // K > 16384: the C ABI routes these to the MFMA GEMM
     }
 }
@@ -778,6 +993,38 @@ hipError_t launch_gemv_q4s(const void *w, const void *xq, float *y, int K, int N
 hipError_t launch_gemv_q4s_fused(const void *w, const float *x, void *xq_out, float *y, int K, int N,
                                  hipStream_t stream) {
     return launch_m<true, 1, JJO_Q4S_U1F, true>(w, x, (uint8_t *)xq_out, y, K, N, stream);
+}
+
+#ifndef JJO_RT_MT4_MAXK_SPLIT
+#define JJO_RT_MT4_MAXK_SPLIT 16384
+#endif
+int gemv_routed_chunk(int max_routes_per_expert, int K, bool split) {
+    const int cap = split && K > JJO_RT_MT4_MAXK_SPLIT ? 2 : 4;
+    const int mt = max_routes_per_expert <= 1 ? 1 : max_routes_per_expert <= 2 ? 2 : 4;
+    return mt < cap ? mt : cap;
+}
+
+hipError_t launch_gemv_routed(const void *w, const void *w2, const void *xq, const int32_t *expert_offsets,
+                              int n_experts, int n_routes, int max_routes_per_expert, float *y, int ldy, int K, int N,
+                              bool split, hipStream_t stream) {
+    if (K > 16384 || max_routes_per_expert < 1) return hipErrorInvalidValue;
+    const int mt = gemv_routed_chunk(max_routes_per_expert, K, split);
+    const int slots = n_experts < n_routes ? n_experts : n_routes;
+    const RouteArgs ra{expert_offsets, (const uint8_t *)w2, n_experts, n_routes, slots, ldy};
+    const int gy = slots * (w2 != nullptr ? 2 : 1);
+    const int gz = (max_routes_per_expert + mt - 1) / mt;
+    if (split) {
+        switch (mt) {
+            case 1: return launch_m<true, 1, JJO_Q4S_U1, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy, gz);
+            case 2: return launch_m<true, 2, 2, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy, gz);
+            default: return launch_m<true, 4, 4, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy, gz);
+        }
+    }
+    switch (mt) {
+        case 1: return launch_m<false, 1, kU1, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy, gz);
+        case 2: return launch_m<false, 2, 2, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy, gz);
+        default: return launch_m<false, 4, kU4, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy, gz);
+    }
 }
 
 }  // namespace jjo

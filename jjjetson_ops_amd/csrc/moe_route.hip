@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include "q4q8_common.hpp"
+#include "q8_1_quant.hpp"
 
 namespace jjo {
 namespace {
@@ -24,12 +25,10 @@ namespace {
 // the 32-lane xor butterfly of warp_reduce_xor_sum (include/cuda_utils.cuh:37-43)
 // over e_0..e_{top_k-1} placed in lanes 0..top_k-1 (zeros elsewhere), so the
 // association order is the reference's; w_i = e_i * (1 / sum).
-__global__ __launch_bounds__(64) void moe_top_k_kernel(const float *__restrict__ logits,
-                                                       float *__restrict__ weights, int *__restrict__ ids,
-                                                       int num_tokens, int num_experts, int top_k) {
-    const int t = blockIdx.x * 64 + threadIdx.x;
-    if (t >= num_tokens) return;
-    const float *row = logits + (size_t)t * num_experts;
+// One token: writes its top_k ids and weights (selection order) to ids[0..top_k)
+// and weights[0..top_k).
+__device__ __forceinline__ void top_k_token(const float *__restrict__ row, int num_experts, int top_k,
+                                            float *__restrict__ weights, int *__restrict__ ids) {
     float sel[32];
     int sel_id[32];
     for (int k = 0; k < top_k; ++k) {
@@ -65,9 +64,18 @@ __global__ __launch_bounds__(64) void moe_top_k_kernel(const float *__restrict__
     }
     const float inv_sum = 1.0f / tree[0];
     for (int k = 0; k < top_k; ++k) {
-        weights[(size_t)t * top_k + k] = lanes[k] * inv_sum;
-        ids[(size_t)t * top_k + k] = sel_id[k];
+        weights[k] = lanes[k] * inv_sum;
+        ids[k] = sel_id[k];
     }
+}
+
+__global__ __launch_bounds__(64) void moe_top_k_kernel(const float *__restrict__ logits,
+                                                       float *__restrict__ weights, int *__restrict__ ids,
+                                                       int num_tokens, int num_experts, int top_k) {
+    const int t = blockIdx.x * 64 + threadIdx.x;
+    if (t >= num_tokens) return;
+    top_k_token(logits + (size_t)t * num_experts, num_experts, top_k, weights + (size_t)t * top_k,
+                ids + (size_t)t * top_k);
 }
 
 // ---------------------------------------------------------------- dispatch
@@ -152,6 +160,67 @@ __global__ __launch_bounds__(256) void moe_gather_q8_1_kernel(const uint8_t *__r
     *reinterpret_cast<uint4 *>(xp + blk * kQ8BlockBytes + 16 * piece) = v;
 }
 
+// ---------------------------------------------------------------- decode routing
+// Decode batches (at most kMoeDecodeRoutes routes): quantize, top-k, dispatch and
+// gather in one launch.  Workgroup p (one per sorted route position) recomputes
+// the top-k of every token (top_k_token, the same bits as moe_top_k_kernel) and
+// the stable positions
+//   pos(r) = #{r' : e(r') < e(r)} + #{r' < r : e(r') = e(r)}
+// (moe_dispatch_kernel's order), then quantizes the fp32 row of its route's token
+// into Q8_1 row p of xp with the quantizer's group arithmetic (quantize_group8:
+// the bytes launch_quantize_q8_1 + moe_gather_q8_1 give).  Workgroup 0 also
+// writes the routing tables.
+__global__ __launch_bounds__(256) void moe_route_decode_kernel(
+    const float *__restrict__ x, const float *__restrict__ logits, int num_tokens, int hidden, int num_experts,
+    int top_k, float *__restrict__ route_w, int *__restrict__ ids, int32_t *__restrict__ expert_offsets,
+    int32_t *__restrict__ src_route, int32_t *__restrict__ dst_of_route, uint8_t *__restrict__ xp) {
+    __shared__ int s_ids[kMoeDecodeRoutes];
+    __shared__ float s_w[kMoeDecodeRoutes];
+    __shared__ int s_src[kMoeDecodeRoutes];
+    const int R = num_tokens * top_k;
+    const bool lead = blockIdx.x == 0;
+    for (int t = threadIdx.x; t < num_tokens; t += blockDim.x)
+        top_k_token(logits + (size_t)t * num_experts, num_experts, top_k, s_w + t * top_k, s_ids + t * top_k);
+    __syncthreads();
+    for (int r = threadIdx.x; r < R; r += blockDim.x) {
+        // (ids clamped to a valid expert, as in moe_dispatch_kernel: memory safety)
+        const int e = min(max(s_ids[r], 0), num_experts - 1);
+        int pos = 0;
+        for (int j = 0; j < R; ++j) {
+            const int ej = min(max(s_ids[j], 0), num_experts - 1);
+            pos += (ej < e) | ((ej == e) & (j < r));
+        }
+        s_src[pos] = r;
+        if (lead) {
+            dst_of_route[r] = pos;
+            route_w[r] = s_w[r];
+            ids[r] = s_ids[r];
+        }
+    }
+    if (lead) {
+        for (int e = threadIdx.x; e <= num_experts; e += blockDim.x) {
+            int c = 0;
+            for (int j = 0; j < R; ++j) c += min(max(s_ids[j], 0), num_experts - 1) < e;
+            expert_offsets[e] = c;
+        }
+    }
+    __syncthreads();
+    if (lead)
+        for (int r = threadIdx.x; r < R; r += blockDim.x) src_route[r] = s_src[r];
+    const int p = blockIdx.x;
+    const float *row = x + (size_t)(s_src[p] / top_k) * hidden;
+    // hidden % 128 == 0: every 32-lane half-wave is live or idle as a whole
+    for (int i0 = threadIdx.x * 4; i0 < hidden; i0 += blockDim.x * 4) {
+        const float4 v = *reinterpret_cast<const float4 *>(row + i0);
+        uint32_t ds;
+        const uint32_t q = quantize_group8(v.x, v.y, v.z, v.w, &ds);
+        uint8_t *out = xp + ((size_t)(i0 / kQSuper) * R + p) * kQ8BlockBytes;
+        const int iqs = i0 % kQSuper;
+        *reinterpret_cast<uint32_t *>(out + 16 + iqs) = q;
+        if ((iqs & 31) == 0) *reinterpret_cast<uint32_t *>(out + 4 * (iqs / 32)) = ds;
+    }
+}
+
 // ---------------------------------------------------------------- combine
 // y[t][h] = sum over k in order of w[t,k] * expert_out[dst(t,k)][h], acc from 0
 // (moe_combine_sota.cu:21-41).  Four consecutive h per thread.
@@ -198,6 +267,16 @@ hipError_t launch_moe_gather_q8_1(const void *xq, const int32_t *src_route, void
     const int64_t total = (int64_t)n_super * n_routes * (kQ8BlockBytes / 16);
     hipLaunchKernelGGL(moe_gather_q8_1_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
                        (const uint8_t *)xq, src_route, (uint8_t *)xp, num_tokens, n_routes, top_k, n_super);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_route_decode(const float *x, const float *logits, int num_tokens, int hidden, int num_experts,
+                                  int top_k, float *route_w, int *ids, int32_t *expert_offsets, int32_t *src_route,
+                                  int32_t *dst_of_route, void *xp, hipStream_t stream) {
+    if (num_tokens * top_k > kMoeDecodeRoutes || hidden % kQSuper != 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(moe_route_decode_kernel, dim3((unsigned)(num_tokens * top_k)), dim3(256), 0, stream, x,
+                       logits, num_tokens, hidden, num_experts, top_k, route_w, ids, expert_offsets, src_route,
+                       dst_of_route, (uint8_t *)xp);
     return hipGetLastError();
 }
 

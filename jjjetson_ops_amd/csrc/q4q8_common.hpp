@@ -51,6 +51,18 @@ hipError_t launch_gemv_fused(const void *w, const float *x, void *xq_out, float 
 hipError_t launch_gemv_q4s(const void *w, const void *xq, float *y, int K, int N, int M, hipStream_t stream);
 hipError_t launch_gemv_q4s_fused(const void *w, const float *x, void *xq_out, float *y, int K, int N,
                                  hipStream_t stream);
+// Routed GEMV over E stacked [N][K] experts (MoE decode): routes sorted by expert,
+// expert_offsets[E+1], Q8_1 route rows superblock-major over n_routes rows; no
+// expert has more than max_routes_per_expert routes.  Sorted route p's output row
+// starts at y + p * ldy.  w2 (nullable): a second stacked matrix of the same shape,
+// computed in the same launch into columns N..2N-1 of each output row.  K <= 16384;
+// split: both matrices in the split layout (planes over all E * N rows).
+hipError_t launch_gemv_routed(const void *w, const void *w2, const void *xq, const int32_t *expert_offsets,
+                              int n_experts, int n_routes, int max_routes_per_expert, float *y, int ldy, int K, int N,
+                              bool split, hipStream_t stream);
+// Routes per workgroup of launch_gemv_routed (1, 2 or 4): its LDS holds that many
+// activation rows of K values (48 B per 32 values split, 40 B block_q4_0).
+int gemv_routed_chunk(int max_routes_per_expert, int K, bool split);
 // Int8-MFMA GEMM, one wave per 32 rows x 128 tokens; weights in the split layout
 // (split = true, 16-byte aligned) or block_q4_0 rows (4-byte aligned).
 hipError_t launch_gemm_q4s_mfma(const void *w, const void *xq, float *y, int K, int N, int M, bool split,
@@ -94,6 +106,14 @@ hipError_t launch_moe_dispatch(const int *ids, int num_routes, int num_experts, 
                                int32_t *src_route, int32_t *dst_of_route, hipStream_t stream);
 hipError_t launch_moe_gather_q8_1(const void *xq, const int32_t *src_route, void *xp, int num_tokens, int n_routes,
                                   int top_k, int K, hipStream_t stream);
+// Decode batches (num_tokens * top_k <= kMoeDecodeRoutes, hidden % 128 == 0):
+// quantize x, top-k, dispatch and the Q8_1 gather in one launch; the outputs are
+// those of launch_quantize_q8_1 + launch_moe_top_k + launch_moe_dispatch +
+// launch_moe_gather_q8_1 (except the unpermuted Q8_1 x, not written).
+constexpr int kMoeDecodeRoutes = 384;
+hipError_t launch_moe_route_decode(const float *x, const float *logits, int num_tokens, int hidden, int num_experts,
+                                  int top_k, float *route_w, int *ids, int32_t *expert_offsets, int32_t *src_route,
+                                  int32_t *dst_of_route, void *xp, hipStream_t stream);
 hipError_t launch_moe_combine(const float *expert_out, const int32_t *dst_of_route, const float *route_weights,
                               float *y, int num_tokens, int hidden, int top_k, hipStream_t stream);
 // fp32 -> Q4_0 over a flat run of n_blocks 32-value blocks.

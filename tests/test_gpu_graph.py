@@ -62,10 +62,11 @@ def test_graph_matmul_f32(M, dev):
     _replays_match(lambda: capi.mat_mul_f32(w, x, xq, y, K, N, M), [y, xq], dev)
 
 
-def test_graph_moe_ffn(dev):
+@pytest.mark.parametrize("T", [48, 3])  # MFMA tiles; routed GEMVs (decode)
+def test_graph_moe_ffn(T, dev):
     import torch
-    note("graph moe_ffn")
-    T, H, I, E, k = 48, 256, 256, 8, 2
+    note(f"graph moe_ffn T={T}")
+    H, I, E, k = 256, 256, 8, 2
     rng = np.random.default_rng(9)
     wg = torch.from_numpy(np.concatenate([_w(I, H, rng) for _ in range(E)])).to(dev)
     wu = torch.from_numpy(np.concatenate([_w(I, H, rng) for _ in range(E)])).to(dev)
@@ -94,10 +95,11 @@ def test_graph_split_layout_matmul_f32(M, dev):
     _replays_match(lambda: capi.mat_mul_split_f32(ws, x, xq, y, K, N, M), [y, xq], dev)
 
 
-def test_graph_moe_ffn_split_layout(dev):
+@pytest.mark.parametrize("T", [48, 3])
+def test_graph_moe_ffn_split_layout(T, dev):
     import torch
-    note("graph moe_ffn split")
-    T, H, I, E, k = 48, 256, 256, 8, 2
+    note(f"graph moe_ffn split T={T}")
+    H, I, E, k = 256, 256, 8, 2
     rng = np.random.default_rng(19)
     mats = []
     for rows, cols in ((I, H), (I, H), (H, I)):

@@ -122,6 +122,20 @@ MOE_CASES = [  # T, H, I, E, top_k
     (40, 128, 128, 256, 8),    # 256 experts for 320 routes: most get 0..3
     (33, 1024, 384, 8, 2),     # wider hidden size
 ]
+# Decode-sized batches: the FFN runs its expert matrices as routed GEMVs (a
+# token's experts are distinct, so no expert holds more than T routes).
+MOE_DECODE_T = 16  # at least the FFN's routed-GEMV token limit
+MOE_DECODE_CASES = [  # T, H, I, E, top_k
+    (1, 256, 384, 8, 2),       # one route per active expert
+    (2, 512, 256, 16, 4),
+    (3, 128, 128, 256, 8),     # 256 experts: the active-expert scan crosses 4 ballots
+    (4, 1024, 384, 8, 2),
+    (8, 256, 256, 64, 8),      # two route chunks per expert
+    (8, 256, 256, 2, 2),       # every token on both experts: 8 routes each
+    (2, 512, 5120, 4, 2),      # down projection K = 5120: two K slices
+    (1, 9216, 256, 4, 2),      # gate|up K = 9216: three K slices
+    (3, 16384, 128, 3, 1),     # gate|up K = 16384: four K slices
+]
 
 
 def _routing(T, E, top_k, seed, dev):
@@ -318,7 +332,7 @@ def _oracle_ffn(x, lg, wg, wu, wd, top_k):
     return oracle_np.moe_combine(eo, dst, w.reshape(-1), top_k)
 
 
-@pytest.mark.parametrize("T,H,I,E,top_k", MOE_CASES)
+@pytest.mark.parametrize("T,H,I,E,top_k", MOE_CASES + MOE_DECODE_CASES)
 def test_moe_ffn_end_to_end(T, H, I, E, top_k, dev):
     import torch
     note(f"moe_ffn T={T} H={H} I={I} E={E} k={top_k}")
@@ -350,9 +364,11 @@ def test_moe_ffn_end_to_end(T, H, I, E, top_k, dev):
     capi.grouped_mat_mul(d["wd"], mq, off, eo, I, H, R)
     y2 = torch.empty(T * H, dtype=torch.float32, device=dev)
     capi.moe_combine(eo, dst, rw, y2, T, H, top_k)
-    assert np.array_equal(y_ffn, host(y2).reshape(T, H))
-
     ref = _oracle_ffn(x, lg, wg, wu, wd, top_k)
+    if T > MOE_DECODE_T:  # the same kernels as the stage entries: the same bits
+        assert np.array_equal(y_ffn, host(y2).reshape(T, H))
+    else:  # routed GEMVs sum each row in another order than the MFMA tiles
+        np.testing.assert_allclose(host(y2).reshape(T, H), ref, rtol=2e-3, atol=2e-3)
     np.testing.assert_allclose(y_ffn, ref, rtol=2e-3, atol=2e-3)
 
 
@@ -402,9 +418,11 @@ def test_grouped_split_layout(counts, N, dev):
     assert np.array_equal(a, b)
 
 
-@pytest.mark.parametrize("T,H,I,E,top_k", MOE_CASES)
+@pytest.mark.parametrize("T,H,I,E,top_k", MOE_CASES + MOE_DECODE_CASES)
 def test_moe_ffn_split_layout(T, H, I, E, top_k, dev):
-    """The FFN on split-layout expert weights equals the block_q4_0 FFN bit for bit."""
+    """The FFN on split-layout expert weights equals the block_q4_0 FFN bit for bit
+    (MFMA tiles); at decode sizes both match the oracle (the routed GEMVs of the two
+    layouts give each lane other blocks, so their sums differ in the last bits)."""
     import torch
     note(f"moe_ffn split T={T} H={H} I={I} E={E} k={top_k}")
     x, lg, wg, wu, wd = _ffn_inputs(T, H, I, E, 900 + T)
@@ -420,5 +438,10 @@ def test_moe_ffn_split_layout(T, H, I, E, top_k, dev):
     capi.moe_ffn(d["x"], d["lg"], sg, su, sd, y2, T, H, I, E, top_k, ws, split=True)
     a, b = host(y1), host(y2)
     assert np.isfinite(a).all()
-    assert np.array_equal(a, b)
+    if T > MOE_DECODE_T:
+        assert np.array_equal(a, b)
+    else:
+        ref = _oracle_ffn(x, lg, wg, wu, wd, top_k)
+        np.testing.assert_allclose(a.reshape(T, H), ref, rtol=2e-3, atol=2e-3)
+        np.testing.assert_allclose(b.reshape(T, H), ref, rtol=2e-3, atol=2e-3)
 
