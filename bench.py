@@ -218,45 +218,71 @@ def time_moe(dev, steps, warmup):
             "kernel_hbm_frac": alg_bytes / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
-def time_moe_ffn(dev, steps, warmup, split=False):
-    """The whole Q4_0 MoE FFN of the same layer shape (8 experts, top-2, 512 tokens,
+def time_moe_ffn(dev, steps, warmup, split=False, T=512):
+    """The whole Q4_0 MoE FFN of the same layer shape (8 experts, top-2, T tokens,
     H=4096, I=14336): quantize, top-k, dispatch, gate|up, SwiGLU+quantize, down,
-    combine -- seven launches per step (gate|up, SwiGLU and its Q8_1 quantization are one)."""
+    combine -- seven launches per step at T=512 (gate|up, SwiGLU and its Q8_1
+    quantization are one); five at decode sizes (T <= 16: one routing launch, routed
+    GEMVs).  Decode steps read only their active experts (2 x 99 MB at T=1), which
+    the 256 MB MALL could keep between steps: there the step rotates over 4 router
+    logit sets that pick different experts and 2 copies of the weights (1.6 GB per
+    cycle), as consecutive layers of a model would."""
     import torch
     from jjjetson_ops_amd import capi
 
-    E, T, topk, H, I = 8, 512, 2, 4096, 14336
+    E, topk, H, I = 8, 2, 4096, 14336
+    decode = T <= 16
+    copies = 2 if decode else 1
+    sets = []
+    for c in range(copies):
+        wg = torch.cat([make_weights(I, H, 60 + e + 100 * c, dev, 1)[0] for e in range(E)])
+        wu = torch.cat([make_weights(I, H, 70 + e + 100 * c, dev, 1)[0] for e in range(E)])
+        wd = torch.cat([make_weights(H, I, 80 + e + 100 * c, dev, 1)[0] for e in range(E)])
+        if split:  # the load-time repack of each stacked expert matrix
+            def repack(src, rows, k):
+                out = torch.empty_like(src)
+                capi.q4_0_to_split(src, out, rows, k)
+                return out
+            wg, wu, wd = repack(wg, E * I, H), repack(wu, E * I, H), repack(wd, E * H, I)
+        sets.append((wg, wu, wd))
+    torch.cuda.synchronize()
     g = torch.Generator(device="cpu").manual_seed(4)
-    logits = torch.randn(T, E, generator=g).to(dev)
-    wg = torch.cat([make_weights(I, H, 60 + e, dev, 1)[0] for e in range(E)])
-    wu = torch.cat([make_weights(I, H, 70 + e, dev, 1)[0] for e in range(E)])
-    wd = torch.cat([make_weights(H, I, 80 + e, dev, 1)[0] for e in range(E)])
-    if split:  # the load-time repack of each stacked expert matrix
-        def repack(src, rows, k):
-            out = torch.empty_like(src)
-            capi.q4_0_to_split(src, out, rows, k)
-            return out
-        wg, wu, wd = repack(wg, E * I, H), repack(wu, E * I, H), repack(wd, E * H, I)
-        torch.cuda.synchronize()
+    if decode:
+        # logit set j favours experts 2j and 2j+1 for every token
+        base = torch.randn(T, E, generator=g)
+        logit_sets = []
+        for j in range(4):
+            lg = base.clone()
+            lg[:, 2 * j:2 * j + 2] += 8.0
+            logit_sets.append(lg)
+    else:
+        logit_sets = [torch.randn(T, E, generator=g)]
+    active = [len(set(torch.topk(lg, topk, dim=1).indices.flatten().tolist())) for lg in logit_sets]
+    logit_sets = [lg.to(dev) for lg in logit_sets]
     x = make_x(T, H, 46, dev, True)
     y = torch.empty(T * H, dtype=torch.float32, device=dev)
     ws = torch.empty(capi.moe_ffn_workspace_bytes(T, H, I, E, topk), dtype=torch.uint8, device=dev)
+    n_log = len(logit_sets)
 
     def step(i):
-        capi.moe_ffn(x, logits, wg, wu, wd, y, T, H, I, E, topk, ws, split=split)
+        capi.moe_ffn(x, logit_sets[i % n_log], *sets[(i // n_log) % copies], y, T, H, I, E, topk, ws, split=split)
 
     for i in range(warmup):
         step(i)
-    avg = _time_steps(step, steps, 7) / steps
+    launches = 5 if decode else 7
+    avg = _time_steps(step, steps, launches) / steps
     R = T * topk
     ops = 2.0 * R * 3 * I * H
-    wbytes = 3 * E * I * (H // 32) * 18  # 792 MB: every step streams past the MALL
+    per_expert = 3 * I * (H // 32) * 18
+    wbytes = per_expert * sum(active) / len(active)  # active experts' weights per step
     torch.cuda.empty_cache()
-    return {"name": "moe_ffn_q4_0_e8_top2_t512_h4096_i14336" + ("_split" if split else ""), "routes": R,
+    return {"name": f"moe_ffn_q4_0_e8_top2_t{T}_h4096_i14336" + ("_split" if split else ""), "routes": R,
             "H": H, "I": I, "weight_layout": "split" if split else "block_q4_0",
             "us_per_step": avg * 1e3, "TOPS": ops / (avg * 1e-3) / 1e12,
             "mfma_frac": ops / (avg * 1e-3) / 1e12 / INT8_PEAK_TOPS,
-            "weight_GBps": wbytes / (avg * 1e-3) / 1e9, "launches_per_step": 7}
+            "active_experts_per_step": sum(active) / len(active),
+            "weight_GBps": wbytes / (avg * 1e-3) / 1e9, "weight_hbm_frac": wbytes / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "launches_per_step": launches}
 
 def time_read_floor(dev, steps, warmup, nbytes=11008 * (4096 // 32) * 18):
     """The single-launch HBM read floor: one plain coalesced read of the decode GEMV's
@@ -467,6 +493,9 @@ def main():
             res = time_moe_ffn(dev, max(5, args.steps // 20), 2)
         elif args.only == "moe_ffn_split":
             res = time_moe_ffn(dev, max(5, args.steps // 20), 2, split=True)
+        elif args.only.startswith("moe_ffn_t"):  # moe_ffn_t<T>[_split]: decode-sized batch
+            res = time_moe_ffn(dev, max(20, args.steps // 4), 5, split=args.only.endswith("_split"),
+                               T=int(args.only[len("moe_ffn_t"):].split("_")[0]))
         elif args.only == "read_floor":
             res = time_read_floor(dev, args.steps, args.warmup)
         elif args.only == "quantize_q4_0":
@@ -504,6 +533,9 @@ def main():
         configs.append(time_moe(dev, max(10, args.steps // 10), 3))
         log("bench: moe ffn")
         configs.append(time_moe_ffn(dev, max(5, args.steps // 20), 2))
+        for T in (1, 4):
+            log(f"bench: moe ffn decode T={T}")
+            configs.append(time_moe_ffn(dev, max(20, args.steps // 4), 5, split=True, T=T))
         log("bench: single-launch read floor")
         configs.append(time_read_floor(dev, args.steps, args.warmup))
         log("bench: q4_0 repacker kernel")

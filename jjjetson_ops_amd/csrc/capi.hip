@@ -798,7 +798,7 @@ struct MoeWs {
 // read once per chunk of its routes) instead of 128-row MFMA tiles, which leave
 // most of the GPU idle when each expert holds a handful of routes.
 #ifndef JJO_MOE_GEMV_TOKENS
-#define JJO_MOE_GEMV_TOKENS 12
+#define JJO_MOE_GEMV_TOKENS 16
 #endif
 bool moe_decode_path(int T, int H, int I, int top_k) {
     return T <= JJO_MOE_GEMV_TOKENS && T * top_k <= kMoeDecodeRoutes && H <= 16384 && I <= 16384;

@@ -287,9 +287,11 @@ __device__ __forceinline__ void finish_f32(uint8_t *xs, uint8_t *__restrict__ xq
 // expert-sorted Q8_1 route rows (superblock-major over n_routes rows); routes
 // offsets[e]..offsets[e+1]-1 use expert e.  blockIdx.y = which * slots + slot
 // selects the slot-th expert that has routes (which = 1: the second stacked
-// matrix w2, written N columns further along each output row), blockIdx.z the
-// chunk of M of its routes.  Output row p (a sorted route position) starts at
-// y + p * ldy.
+// matrix w2, written N columns further along each output row).  The workgroup
+// keeps its weight rows in registers and takes the expert's routes M at a time
+// (each chunk re-stages only activation rows), so every weight byte of an active
+// expert is read once whatever its route count.  Output row p (a sorted route
+// position) starts at y + p * ldy.
 struct RouteArgs {
     const int32_t *offsets;  // [n_experts + 1]
     const uint8_t *w2;       // second stacked matrix, or null
@@ -297,7 +299,7 @@ struct RouteArgs {
 };
 
 struct RouteTile {
-    int expert, which, m0, mc;  // routes m0 .. m0 + mc - 1 of `expert`
+    int expert, which, m0, mc, end;  // first chunk: routes m0 .. m0 + mc - 1; the expert's end
 };
 
 // Clamped route range of expert e (a malformed table gives fewer routes, never
@@ -332,12 +334,12 @@ __device__ __forceinline__ bool route_tile(const RouteArgs &ra, int mt, RouteTil
     if (e < 0) return false;
     int beg, end;
     expert_range(ra, e, beg, end);
-    const int m0 = beg + (int)blockIdx.z * mt;
-    if (m0 >= end) return false;
+    if (beg >= end) return false;
     t.expert = e;
     t.which = which;
-    t.m0 = m0;
-    t.mc = min(mt, end - m0);
+    t.m0 = beg;
+    t.mc = min(mt, end - beg);
+    t.end = end;
     return true;
 }
 
@@ -357,6 +359,11 @@ __device__ __forceinline__ void issue_q8_routed(ItemQ8 &it, const uint8_t *__res
     const u32x4a16 v1 = *reinterpret_cast<const u32x4a16 *>(blk + 32 + 32 * g);
     it.q[0] = v0.x; it.q[1] = v0.y; it.q[2] = v0.z; it.q[3] = v0.w;
     it.q[4] = v1.x; it.q[5] = v1.y; it.q[6] = v1.z; it.q[7] = v1.w;
+}
+
+__device__ __forceinline__ int opaque_int(int v) {
+    asm volatile("" : "+v"(v));
+    return v;
 }
 
 // Workgroup = RG row groups x JS K-slices (one wave each).  JS = ceil(K / 4096).
@@ -386,13 +393,15 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
     const int r0 = (blockIdx.x * RG + rg) * U;
     const int n_items = FUSED ? 2 * nb : M * nb;
     const int rounds = (n_items + kThreadsWG - 1) / kThreadsWG;
-    RouteTile rt{0, 0, 0, M};
+    RouteTile rt{0, 0, 0, M, M};
     if constexpr (ROUTED) {
         if (!route_tile(ra, M, rt)) return;
         w = (rt.which ? ra.w2 : w) + (size_t)rt.expert * N * row_bytes;
         y += (size_t)rt.m0 * ra.ldy + (size_t)rt.which * N;
     }
     const int ldy = ROUTED ? ra.ldy : N;
+    int m0c = rt.m0, mcc = rt.mc;  // the current chunk of routes (routed launches)
+    bool again = false;            // a later chunk: all its items are loaded in the pass
 
     // All global loads below are unconditional (clamped addresses), so the
     // compiler can count them and wait for exactly the ones each step needs.
@@ -406,7 +415,7 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
             issue_f32(early[r], reinterpret_cast<const float *>(xin), item, nb);
         } else {
             if constexpr (ROUTED)
-                issue_q8_routed<M>(early[r], reinterpret_cast<const uint8_t *>(xin), item, nb, ra.n_routes, rt.m0, rt.mc);
+                issue_q8_routed<M>(early[r], reinterpret_cast<const uint8_t *>(xin), item, nb, ra.n_routes, m0c, mcc);
             else
                 issue_q8<M>(early[r], reinterpret_cast<const uint8_t *>(xin), item, nb);
         }
@@ -424,7 +433,8 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    // 3) activation planes of the whole K range in LDS, once per workgroup
+    // 3) the early items (routed launches: before the chunk loop, so that they are not
+    //    held across it; later chunks load every item in their pass)
     uint8_t *xq_w = (FUSED && blockIdx.x == 0) ? xq_out : nullptr;
 #pragma unroll
     for (int r = 0; r < EARLY; ++r) {
@@ -435,128 +445,176 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
             finish_q8(xs, early[r], item, nb, n_items);
         }
     }
-    for (int r = EARLY; r < rounds; ++r) {  // long activations: the rest, load-then-use
-        const int item = threadIdx.x + r * kThreadsWG;
-        Item it;
-        if constexpr (FUSED) {
-            issue_f32(it, reinterpret_cast<const float *>(xin), item, nb);
-            finish_f32(xs, xq_w, it, item, nb, item < n_items);
-        } else {
-            if constexpr (ROUTED)
-                issue_q8_routed<M>(it, reinterpret_cast<const uint8_t *>(xin), item, nb, ra.n_routes, rt.m0, rt.mc);
-            else
-                issue_q8<M>(it, reinterpret_cast<const uint8_t *>(xin), item, nb);
-            finish_q8(xs, it, item, nb, n_items);
-        }
-    }
-    __syncthreads();
-
-    // 4) rows in load order: the wait for row u covers only rows 0..u
-    float acc[U][M];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int m = 0; m < M; ++m) acc[u][m] = 0.0f;
-
-    if (ROUTED && live) {
-        // Token-outer: tokens past this expert's routes (mc <= M, uniform over the
-        // workgroup) cost no dot products; each (row, token) sum is the same
-        // expression as below.
-        uint32_t qa[U][4], qb[U][4];
-        int32_t na[U], nbs[U];
-        float dwa[U], dwb[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                qa[u][i] = __builtin_amdgcn_alignbyte(wb[u].d[i + 1], wb[u].d[i], 2);
-                qb[u][i] = wb[u].d[i + 5];
+    const int lane_o = lane, js_o = js, rg_o = rg, p_o = p, r0_o = r0;  // (see the pass)
+    for (;;) {  // one pass; routed launches: one per chunk of routes
+        // Routed launches recompute the lane values of each pass from an opaque
+        // thread index instead of holding them (and what derives from them) across
+        // passes, which would cost the 1- and 2-route kernels half their occupancy.
+        const int tid = ROUTED ? opaque_int(threadIdx.x) : (int)threadIdx.x;
+        const int lane = ROUTED ? (tid & 63) : lane_o;
+        const int js = ROUTED ? (tid >> 6) % JS : js_o;
+        const int rg = ROUTED ? (tid >> 6) / JS : rg_o;
+        const int p = ROUTED ? lane + 64 * js : p_o;
+        const bool live = p < P;
+        const int r0 = ROUTED ? (int)(blockIdx.x * RG + rg) * U : r0_o;
+        // 3) activation planes of the whole K range in LDS, once per workgroup (routed:
+        //    per chunk of routes)
+        for (int r = (ROUTED && again) ? 0 : EARLY; r < rounds; ++r) {  // the rest, load-then-use
+            const int item = tid + r * kThreadsWG;
+            Item it;
+            if constexpr (FUSED) {
+                issue_f32(it, reinterpret_cast<const float *>(xin), item, nb);
+                finish_f32(xs, xq_w, it, item, nb, item < n_items);
+            } else {
+                if constexpr (ROUTED)
+                    issue_q8_routed<M>(it, reinterpret_cast<const uint8_t *>(xin), item, nb, ra.n_routes, m0c, mcc);
+                else
+                    issue_q8<M>(it, reinterpret_cast<const uint8_t *>(xin), item, nb);
+                finish_q8(xs, it, item, nb, n_items);
             }
-            na[u] = nib_sum128(qa[u]);
-            nbs[u] = nib_sum128(qb[u]);
-            dwa[u] = half_lo(wb[u].d[0]);
-            dwb[u] = half_hi(wb[u].d[4]);
         }
+        __syncthreads();
+
+        // 4) rows in load order: the wait for row u covers only rows 0..u
+        float acc[U][M];
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-            if (m < rt.mc) {
-                const uint8_t *rec = xs + ((size_t)m * P + p) * kRec;
-                const u32x4a16 ha = *reinterpret_cast<const u32x4a16 *>(rec);
-                const u32x4a16 la = *reinterpret_cast<const u32x4a16 *>(rec + 16);
-                const u32x4a16 hb = *reinterpret_cast<const u32x4a16 *>(rec + 32);
-                const u32x4a16 lb = *reinterpret_cast<const u32x4a16 *>(rec + 48);
-                const f32x4 cst = *reinterpret_cast<const f32x4 *>(rec + 64);
-                const uint32_t hia[4] = {ha.x, ha.y, ha.z, ha.w}, loa[4] = {la.x, la.y, la.z, la.w};
-                const uint32_t hib[4] = {hb.x, hb.y, hb.z, hb.w}, lob[4] = {lb.x, lb.y, lb.z, lb.w};
+        for (int u = 0; u < U; ++u)
 #pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const int32_t sa = block_sumi(qa[u], hia, loa, na[u]);
-                    const int32_t sb = block_sumi(qb[u], hib, lob, nbs[u]);
-                    float a = dwa[u] * fmaf((float)sa, cst.x, cst.y);
-                    a = fmaf(dwb[u], fmaf((float)sb, cst.z, cst.w), a);
+            for (int m = 0; m < M; ++m) acc[u][m] = 0.0f;
+
+        if (ROUTED && live) {
+            // Token-outer: tokens past this expert's routes (mc <= M, uniform over the
+            // workgroup) cost no dot products; each (row, token) sum is the same
+            // expression as below.
+            // Per row: the nibble sums and scales; the nibble dwords themselves are
+            // taken from wb per token (block b's are 2-byte shifted: one alignbyte
+            // each), which keeps the pass under the 1024-thread register budget.
+            int32_t na[U], nbs[U];
+            float dwa[U], dwb[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                // Opaque per pass: the weight terms below stay after the activation
+                // staging instead of being hoisted ahead of it (which would wait on
+                // every weight load before the first LDS write).
+#pragma unroll
+                for (int i = 0; i < 9; ++i) asm volatile("" : "+v"(wb[u].d[i]));
+                uint32_t qa[4], qb[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    qa[i] = __builtin_amdgcn_alignbyte(wb[u].d[i + 1], wb[u].d[i], 2);
+                    qb[i] = wb[u].d[i + 5];
+                }
+                na[u] = nib_sum128(qa);
+                nbs[u] = nib_sum128(qb);
+                dwa[u] = half_lo(wb[u].d[0]);
+                dwb[u] = half_hi(wb[u].d[4]);
+            }
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                if (m < mcc) {
+                    const uint8_t *rec = xs + ((size_t)m * P + p) * kRec;
+                    const u32x4a16 ha = *reinterpret_cast<const u32x4a16 *>(rec);
+                    const u32x4a16 la = *reinterpret_cast<const u32x4a16 *>(rec + 16);
+                    const u32x4a16 hb = *reinterpret_cast<const u32x4a16 *>(rec + 32);
+                    const u32x4a16 lb = *reinterpret_cast<const u32x4a16 *>(rec + 48);
+                    const f32x4 cst = *reinterpret_cast<const f32x4 *>(rec + 64);
+                    const uint32_t hia[4] = {ha.x, ha.y, ha.z, ha.w}, loa[4] = {la.x, la.y, la.z, la.w};
+                    const uint32_t hib[4] = {hb.x, hb.y, hb.z, hb.w}, lob[4] = {lb.x, lb.y, lb.z, lb.w};
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+                        uint32_t qa[4], qb[4];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            qa[i] = __builtin_amdgcn_alignbyte(wb[u].d[i + 1], wb[u].d[i], 2);
+                            qb[i] = wb[u].d[i + 5];
+                        }
+                        const int32_t sa = block_sumi(qa, hia, loa, na[u]);
+                        const int32_t sb = block_sumi(qb, hib, lob, nbs[u]);
+                        float a = dwa[u] * fmaf((float)sa, cst.x, cst.y);
+                        a = fmaf(dwb[u], fmaf((float)sb, cst.z, cst.w), a);
+                        acc[u][m] = a;
+                    }
+                }
+            }
+        } else if (live) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                uint32_t qa[4], qb[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    qa[i] = __builtin_amdgcn_alignbyte(wb[u].d[i + 1], wb[u].d[i], 2);
+                    qb[i] = wb[u].d[i + 5];
+                }
+                const int32_t na = nib_sum128(qa), nbs = nib_sum128(qb);
+                const float dwa = half_lo(wb[u].d[0]);
+                const float dwb = half_hi(wb[u].d[4]);
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const uint8_t *rec = xs + ((size_t)m * P + p) * kRec;
+                    const u32x4a16 ha = *reinterpret_cast<const u32x4a16 *>(rec);
+                    const u32x4a16 la = *reinterpret_cast<const u32x4a16 *>(rec + 16);
+                    const u32x4a16 hb = *reinterpret_cast<const u32x4a16 *>(rec + 32);
+                    const u32x4a16 lb = *reinterpret_cast<const u32x4a16 *>(rec + 48);
+                    const f32x4 cst = *reinterpret_cast<const f32x4 *>(rec + 64);
+                    const uint32_t hia[4] = {ha.x, ha.y, ha.z, ha.w}, loa[4] = {la.x, la.y, la.z, la.w};
+                    const uint32_t hib[4] = {hb.x, hb.y, hb.z, hb.w}, lob[4] = {lb.x, lb.y, lb.z, lb.w};
+                    const int32_t sa = block_sumi(qa, hia, loa, na);
+                    const int32_t sb = block_sumi(qb, hib, lob, nbs);
+                    float a = dwa * fmaf((float)sa, cst.x, cst.y);
+                    a = fmaf(dwb, fmaf((float)sb, cst.z, cst.w), a);
                     acc[u][m] = a;
                 }
             }
         }
-    } else if (live) {
+
+        // All U * M sums of the wave in one transposed reduction; lane `owner` of each
+        // group that shares a value holds its sum.
+        constexpr int NV = pow2_at_least(U * M);
+        float v[NV];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            uint32_t qa[4], qb[4];
+        for (int i = 0; i < NV; ++i) v[i] = i < U * M ? acc[i / M][i % M] : 0.0f;
+        const float s = multi_sum<NV>(v, lane);
+        const int idx = multi_sum_index<NV>(lane);
+        const int u = idx / M, m = idx % M;
+        const bool owner = (lane & (64 / NV - 1)) == 0 && idx < U * M;
+        if constexpr (JS == 1) {
+            if (owner && r0 + u < N) if (m < mcc) y[(size_t)m * ldy + r0 + u] = s;
+        } else {
+            if (owner) part[((rg * U + u) * M + m) * JS + js] = s;
+            __syncthreads();
+            if (js == 0) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                qa[i] = __builtin_amdgcn_alignbyte(wb[u].d[i + 1], wb[u].d[i], 2);
-                qb[i] = wb[u].d[i + 5];
-            }
-            const int32_t na = nib_sum128(qa), nbs = nib_sum128(qb);
-            const float dwa = half_lo(wb[u].d[0]);
-            const float dwb = half_hi(wb[u].d[4]);
+                for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int m = 0; m < M; ++m) {
-                const uint8_t *rec = xs + ((size_t)m * P + p) * kRec;
-                const u32x4a16 ha = *reinterpret_cast<const u32x4a16 *>(rec);
-                const u32x4a16 la = *reinterpret_cast<const u32x4a16 *>(rec + 16);
-                const u32x4a16 hb = *reinterpret_cast<const u32x4a16 *>(rec + 32);
-                const u32x4a16 lb = *reinterpret_cast<const u32x4a16 *>(rec + 48);
-                const f32x4 cst = *reinterpret_cast<const f32x4 *>(rec + 64);
-                const uint32_t hia[4] = {ha.x, ha.y, ha.z, ha.w}, loa[4] = {la.x, la.y, la.z, la.w};
-                const uint32_t hib[4] = {hb.x, hb.y, hb.z, hb.w}, lob[4] = {lb.x, lb.y, lb.z, lb.w};
-                const int32_t sa = block_sumi(qa, hia, loa, na);
-                const int32_t sb = block_sumi(qb, hib, lob, nbs);
-                float a = dwa * fmaf((float)sa, cst.x, cst.y);
-                a = fmaf(dwb, fmaf((float)sb, cst.z, cst.w), a);
-                acc[u][m] = a;
+                    for (int m = 0; m < M; ++m) {
+                        if (lane == ((u * M + m) & 63) && r0 + u < N) {
+                            const float *pp = part + ((rg * U + u) * M + m) * JS;
+                            float s = pp[0];
+#pragma unroll
+                            for (int j = 1; j < JS; ++j) s += pp[j];
+                            if (m < mcc) y[(size_t)m * ldy + r0 + u] = s;
+                        }
+                    }
             }
         }
-    }
-
-    // All U * M sums of the wave in one transposed reduction; lane `owner` of each
-    // group that shares a value holds its sum.
-    constexpr int NV = pow2_at_least(U * M);
-    float v[NV];
-#pragma unroll
-    for (int i = 0; i < NV; ++i) v[i] = i < U * M ? acc[i / M][i % M] : 0.0f;
-    const float s = multi_sum<NV>(v, lane);
-    const int idx = multi_sum_index<NV>(lane);
-    const int u = idx / M, m = idx % M;
-    const bool owner = (lane & (64 / NV - 1)) == 0 && idx < U * M;
-    if constexpr (JS == 1) {
-        if (owner && r0 + u < N) if (m < rt.mc) y[(size_t)m * ldy + r0 + u] = s;
-    } else {
-        if (owner) part[((rg * U + u) * M + m) * JS + js] = s;
-        __syncthreads();
-        if (js == 0) {
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-#pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    if (lane == ((u * M + m) & 63) && r0 + u < N) {
-                        const float *pp = part + ((rg * U + u) * M + m) * JS;
-                        float s = pp[0];
-#pragma unroll
-                        for (int j = 1; j < JS; ++j) s += pp[j];
-                        if (m < rt.mc) y[(size_t)m * ldy + r0 + u] = s;
-                    }
-                }
+        if constexpr (!ROUTED) {
+            break;
+        } else {
+            // the expert's next chunk of routes: the same weight rows, new activation rows
+            m0c += M;
+            if (m0c >= rt.end) break;
+            mcc = min(M, rt.end - m0c);
+            y += (size_t)M * ldy;
+            again = true;
+            __syncthreads();  // every wave is done with the records and partial sums
+            if constexpr (M <= 2) {
+                // Re-request the weight rows (L2) rather than keep them live through
+                // the pass: held, they cost the 1- and 2-route kernels half their
+                // occupancy, for a loop that only a tie-broken top-k repeat reaches.
+                const int pl = min(p, P - 1);
+                for (int u = 0; u < U; ++u)
+                    load_pair(wb[u], w + (size_t)min(r0 + u, N - 1) * row_bytes + (size_t)pl * 36);
+            }
         }
     }
 }
@@ -673,7 +731,7 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
     const int r0 = (blockIdx.x * RG + rg) * U;
     const int n_items = FUSED ? 2 * nb : M * nb;
     const int rounds = (n_items + kThreadsWG - 1) / kThreadsWG;
-    RouteTile rt{0, 0, 0, M};
+    RouteTile rt{0, 0, 0, M, M};
     size_t plane_rows = N, row0 = 0;  // rows of the buffer's planes, first row of this matrix
     if constexpr (ROUTED) {
         if (!route_tile(ra, M, rt)) return;
@@ -683,6 +741,8 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
         y += (size_t)rt.m0 * ra.ldy + (size_t)rt.which * N;
     }
     const int ldy = ROUTED ? ra.ldy : N;
+    int m0c = rt.m0, mcc = rt.mc;  // the current chunk of routes (routed launches)
+    bool again = false;            // a later chunk: all its items are loaded in the pass
     const uint16_t *__restrict__ dpl = reinterpret_cast<const uint16_t *>(w + plane_rows * nb * 16);
 
     // 1) activation requests (L2-resident), ahead of the weights
@@ -695,7 +755,7 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
             issue_f32(early[r], reinterpret_cast<const float *>(xin), item, nb);
         } else {
             if constexpr (ROUTED)
-                issue_q8_routed<M>(early[r], reinterpret_cast<const uint8_t *>(xin), item, nb, ra.n_routes, rt.m0, rt.mc);
+                issue_q8_routed<M>(early[r], reinterpret_cast<const uint8_t *>(xin), item, nb, ra.n_routes, m0c, mcc);
             else
                 issue_q8<M>(early[r], reinterpret_cast<const uint8_t *>(xin), item, nb);
         }
@@ -713,7 +773,8 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
         wd[u][1] = dpl[base + c1];
     }
     __builtin_amdgcn_sched_barrier(0);
-    // 3) activation records of the whole K range in LDS, once per workgroup
+    // 3) the early items (routed launches: before the chunk loop, so that they are not
+    //    held across it; later chunks load every item in their pass)
     uint8_t *xq_w = (FUSED && blockIdx.x == 0) ? xq_out : nullptr;
 #pragma unroll
     for (int r = 0; r < EARLY; ++r) {
@@ -724,114 +785,151 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
             finish_q8_s(xs, early[r], item, nb, n_items);
         }
     }
-    for (int r = EARLY; r < rounds; ++r) {
-        const int item = threadIdx.x + r * kThreadsWG;
-        Item it;
-        if constexpr (FUSED) {
-            issue_f32(it, reinterpret_cast<const float *>(xin), item, nb);
-            finish_f32_s(xs, xq_w, it, item, nb, item < n_items);
-        } else {
-            if constexpr (ROUTED)
-                issue_q8_routed<M>(it, reinterpret_cast<const uint8_t *>(xin), item, nb, ra.n_routes, rt.m0, rt.mc);
-            else
-                issue_q8<M>(it, reinterpret_cast<const uint8_t *>(xin), item, nb);
-            finish_q8_s(xs, it, item, nb, n_items);
+    const int lane_o = lane, js_o = js, rg_o = rg, bk0_o = bk0, r0_o = r0;  // (see the pass)
+    for (;;) {  // one pass; routed launches: one per chunk of routes
+        // (lane values per pass: as in gemv_q4_0_q8_1_kernel)
+        const int tid = ROUTED ? opaque_int(threadIdx.x) : (int)threadIdx.x;
+        const int lane = ROUTED ? (tid & 63) : lane_o;
+        const int js = ROUTED ? (tid >> 6) % JS : js_o;
+        const int rg = ROUTED ? (tid >> 6) / JS : rg_o;
+        const int bk0 = ROUTED ? 128 * js + lane : bk0_o;
+        const int bk1 = bk0 + 64;
+        const int c0 = min(bk0, nb - 1), c1 = min(bk1, nb - 1);
+        const int r0 = ROUTED ? (int)(blockIdx.x * RG + rg) * U : r0_o;
+        // 3) activation records of the whole K range in LDS, once per workgroup (routed:
+        //    per chunk of routes)
+        for (int r = (ROUTED && again) ? 0 : EARLY; r < rounds; ++r) {  // the rest, load-then-use
+            const int item = tid + r * kThreadsWG;
+            Item it;
+            if constexpr (FUSED) {
+                issue_f32(it, reinterpret_cast<const float *>(xin), item, nb);
+                finish_f32_s(xs, xq_w, it, item, nb, item < n_items);
+            } else {
+                if constexpr (ROUTED)
+                    issue_q8_routed<M>(it, reinterpret_cast<const uint8_t *>(xin), item, nb, ra.n_routes, m0c, mcc);
+                else
+                    issue_q8<M>(it, reinterpret_cast<const uint8_t *>(xin), item, nb);
+                finish_q8_s(xs, it, item, nb, n_items);
+            }
         }
-    }
-    __syncthreads();
+        __syncthreads();
 
-    // 4) rows in load order
-    float acc[U][M];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-#pragma unroll
-        for (int m = 0; m < M; ++m) acc[u][m] = 0.0f;
-
-    if constexpr (ROUTED) {
-        // Token-outer (as in gemv_q4_0_q8_1_kernel): tokens past the expert's routes
-        // cost no dot products; every sum adds block k = 0, then k = 1, as below.
-        int32_t ns[U][2];
-        float dw[U][2];
+        // 4) rows in load order
+        float acc[U][M];
 #pragma unroll
         for (int u = 0; u < U; ++u)
 #pragma unroll
-            for (int k = 0; k < 2; ++k) {
-                const uint32_t q[4] = {wq[u][k].x, wq[u][k].y, wq[u][k].z, wq[u][k].w};
-                ns[u][k] = nib_sum128(q);
-                dw[u][k] = __half2float(__ushort_as_half((unsigned short)wd[u][k]));
-            }
+            for (int m = 0; m < M; ++m) acc[u][m] = 0.0f;
+
+        if constexpr (ROUTED) {
+            // Token-outer (as in gemv_q4_0_q8_1_kernel): tokens past the expert's routes
+            // cost no dot products; every sum adds block k = 0, then k = 1, as below.
+            int32_t ns[U][2];
+            float dw[U][2];
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-            if (m < rt.mc) {
+            for (int u = 0; u < U; ++u)
 #pragma unroll
                 for (int k = 0; k < 2; ++k) {
-                    const bool live = (k ? bk1 : bk0) < nb;
-                    const uint8_t *rec = xs + ((size_t)m * nb + (k ? c1 : c0)) * kRecS;
+                    // opaque per pass: keeps the weight terms after the staging (as in
+                    // gemv_q4_0_q8_1_kernel)
+                    asm volatile("" : "+v"(wq[u][k]), "+v"(wd[u][k]));
+                    const uint32_t q[4] = {wq[u][k].x, wq[u][k].y, wq[u][k].z, wq[u][k].w};
+                    ns[u][k] = nib_sum128(q);
+                    dw[u][k] = __half2float(__ushort_as_half((unsigned short)wd[u][k]));
+                }
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                if (m < mcc) {
+#pragma unroll
+                    for (int k = 0; k < 2; ++k) {
+                        const bool live = (k ? bk1 : bk0) < nb;
+                        const uint8_t *rec = xs + ((size_t)m * nb + (k ? c1 : c0)) * kRecS;
+                        const u32x4a16 h4 = *reinterpret_cast<const u32x4a16 *>(rec);
+                        const u32x4a16 l4 = *reinterpret_cast<const u32x4a16 *>(rec + 16);
+                        const u32x2a8 c2 = *reinterpret_cast<const u32x2a8 *>(rec + 32);
+                        const uint32_t hi[4] = {h4.x, h4.y, h4.z, h4.w}, lo[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+                        for (int u = 0; u < U; ++u) {
+                            const uint32_t q[4] = {wq[u][k].x, wq[u][k].y, wq[u][k].z, wq[u][k].w};
+                            const int32_t sv = block_sumi(q, hi, lo, ns[u][k]);
+                            const float v = dw[u][k] * fmaf((float)sv, __uint_as_float(c2.x), __uint_as_float(c2.y));
+                            acc[u][m] += live ? v : 0.0f;
+                        }
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const bool live = (k ? bk1 : bk0) < nb;
+                const int cb = k ? c1 : c0;
+                const uint32_t q[4] = {wq[u][k].x, wq[u][k].y, wq[u][k].z, wq[u][k].w};
+                const int32_t ns = nib_sum128(q);
+                const float dw = __half2float(__ushort_as_half((unsigned short)wd[u][k]));
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const uint8_t *rec = xs + ((size_t)m * nb + cb) * kRecS;
                     const u32x4a16 h4 = *reinterpret_cast<const u32x4a16 *>(rec);
                     const u32x4a16 l4 = *reinterpret_cast<const u32x4a16 *>(rec + 16);
                     const u32x2a8 c2 = *reinterpret_cast<const u32x2a8 *>(rec + 32);
                     const uint32_t hi[4] = {h4.x, h4.y, h4.z, h4.w}, lo[4] = {l4.x, l4.y, l4.z, l4.w};
-#pragma unroll
-                    for (int u = 0; u < U; ++u) {
-                        const uint32_t q[4] = {wq[u][k].x, wq[u][k].y, wq[u][k].z, wq[u][k].w};
-                        const int32_t sv = block_sumi(q, hi, lo, ns[u][k]);
-                        const float v = dw[u][k] * fmaf((float)sv, __uint_as_float(c2.x), __uint_as_float(c2.y));
-                        acc[u][m] += live ? v : 0.0f;
-                    }
+                    const int32_t sv = block_sumi(q, hi, lo, ns);
+                    const float v = dw * fmaf((float)sv, __uint_as_float(c2.x), __uint_as_float(c2.y));
+                    acc[u][m] += live ? v : 0.0f;
                 }
             }
         }
-    } else {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            const bool live = (k ? bk1 : bk0) < nb;
-            const int cb = k ? c1 : c0;
-            const uint32_t q[4] = {wq[u][k].x, wq[u][k].y, wq[u][k].z, wq[u][k].w};
-            const int32_t ns = nib_sum128(q);
-            const float dw = __half2float(__ushort_as_half((unsigned short)wd[u][k]));
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-                const uint8_t *rec = xs + ((size_t)m * nb + cb) * kRecS;
-                const u32x4a16 h4 = *reinterpret_cast<const u32x4a16 *>(rec);
-                const u32x4a16 l4 = *reinterpret_cast<const u32x4a16 *>(rec + 16);
-                const u32x2a8 c2 = *reinterpret_cast<const u32x2a8 *>(rec + 32);
-                const uint32_t hi[4] = {h4.x, h4.y, h4.z, h4.w}, lo[4] = {l4.x, l4.y, l4.z, l4.w};
-                const int32_t sv = block_sumi(q, hi, lo, ns);
-                const float v = dw * fmaf((float)sv, __uint_as_float(c2.x), __uint_as_float(c2.y));
-                acc[u][m] += live ? v : 0.0f;
-            }
         }
-    }
-    }
 
-    constexpr int NV = pow2_at_least(U * M);
-    float v[NV];
+        constexpr int NV = pow2_at_least(U * M);
+        float v[NV];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) v[i] = i < U * M ? acc[i / M][i % M] : 0.0f;
-    const float s = multi_sum<NV>(v, lane);
-    const int idx = multi_sum_index<NV>(lane);
-    const int u = idx / M, m = idx % M;
-    const bool owner = (lane & (64 / NV - 1)) == 0 && idx < U * M;
-    if constexpr (JS == 1) {
-        if (owner && r0 + u < N) if (m < rt.mc) y[(size_t)m * ldy + r0 + u] = s;
-    } else {
-        if (owner) part[((rg * U + u) * M + m) * JS + js] = s;
-        __syncthreads();
-        if (js == 0) {
+        for (int i = 0; i < NV; ++i) v[i] = i < U * M ? acc[i / M][i % M] : 0.0f;
+        const float s = multi_sum<NV>(v, lane);
+        const int idx = multi_sum_index<NV>(lane);
+        const int u = idx / M, m = idx % M;
+        const bool owner = (lane & (64 / NV - 1)) == 0 && idx < U * M;
+        if constexpr (JS == 1) {
+            if (owner && r0 + u < N) if (m < mcc) y[(size_t)m * ldy + r0 + u] = s;
+        } else {
+            if (owner) part[((rg * U + u) * M + m) * JS + js] = s;
+            __syncthreads();
+            if (js == 0) {
 #pragma unroll
-            for (int u = 0; u < U; ++u)
+                for (int u = 0; u < U; ++u)
 #pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    if (lane == ((u * M + m) & 63) && r0 + u < N) {
-                        const float *pp = part + ((rg * U + u) * M + m) * JS;
-                        float s = pp[0];
+                    for (int m = 0; m < M; ++m) {
+                        if (lane == ((u * M + m) & 63) && r0 + u < N) {
+                            const float *pp = part + ((rg * U + u) * M + m) * JS;
+                            float s = pp[0];
 #pragma unroll
-                        for (int j = 1; j < JS; ++j) s += pp[j];
-                        if (m < rt.mc) y[(size_t)m * ldy + r0 + u] = s;
+                            for (int j = 1; j < JS; ++j) s += pp[j];
+                            if (m < mcc) y[(size_t)m * ldy + r0 + u] = s;
+                        }
                     }
+            }
+        }
+        if constexpr (!ROUTED) {
+            break;
+        } else {
+            // the expert's next chunk of routes: the same weight rows, new activation rows
+            m0c += M;
+            if (m0c >= rt.end) break;
+            mcc = min(M, rt.end - m0c);
+            y += (size_t)M * ldy;
+            again = true;
+            __syncthreads();  // every wave is done with the records and partial sums
+            if constexpr (M <= 2) {  // (as in gemv_q4_0_q8_1_kernel)
+                for (int u = 0; u < U; ++u) {
+                    const size_t base = (row0 + (size_t)min(r0 + u, N - 1)) * nb;
+                    wq[u][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4a16 *>(w + (base + c0) * 16));
+                    wq[u][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4a16 *>(w + (base + c1) * 16));
+                    wd[u][0] = dpl[base + c0];
+                    wd[u][1] = dpl[base + c1];
                 }
+            }
         }
     }
 }
@@ -887,18 +985,21 @@ constexpr int rg_for_s() {
 #ifndef JJO_RT_RG4
 #define JJO_RT_RG4 4
 #endif
+#ifndef JJO_RT_RG4_BLK_M4
+#define JJO_RT_RG4_BLK_M4 4
+#endif
 template <bool SPLIT, int M, int JS, bool FUSED, bool ROUTED>
 constexpr int rg_pick() {
     if (ROUTED && JS == 2) return JJO_RT_RG2;
     if (ROUTED && JS == 3) return JJO_RT_RG3;
-    if (ROUTED && JS == 4) return JJO_RT_RG4;
+    if (ROUTED && JS == 4) return (!SPLIT && M == 4) ? JJO_RT_RG4_BLK_M4 : JJO_RT_RG4;
     return SPLIT ? rg_for_s<M, JS, FUSED>() : rg_for<M, JS, FUSED>();
 }
 
-// Routed launches (ROUTED) run gz token chunks over the gy expert slots of `ra`.
+// Routed launches (ROUTED) run over the gy expert slots of `ra`.
 template <bool SPLIT, int M, int U, int JS, bool FUSED, int EARLY, bool ROUTED = false>
 hipError_t launch_cfg(const void *w, const void *xin, uint8_t *xq_out, float *y, int K, int N, hipStream_t stream,
-                      const RouteArgs &ra = RouteArgs{}, int gy = 1, int gz = 1) {
+                      const RouteArgs &ra = RouteArgs{}, int gy = 1) {
     constexpr int RG = rg_pick<SPLIT, M, JS, FUSED, ROUTED>();
     const int groups = (N + U - 1) / U;
     const int blocks = (groups + RG - 1) / RG;
@@ -911,10 +1012,10 @@ hipError_t launch_cfg(const void *w, const void *xin, uint8_t *xq_out, float *y,
         if (e != hipSuccess) return e;
     }
     if constexpr (SPLIT) {
-        hipLaunchKernelGGL((gemv_q4s_kernel<M, U, JS, RG, FUSED, EARLY, ROUTED>), dim3(blocks, gy, gz),
+        hipLaunchKernelGGL((gemv_q4s_kernel<M, U, JS, RG, FUSED, EARLY, ROUTED>), dim3(blocks, gy),
                            dim3(64 * JS * RG), smem, stream, (const uint8_t *)w, xin, xq_out, y, K, N, ra);
     } else {
-        hipLaunchKernelGGL((gemv_q4_0_q8_1_kernel<M, U, JS, RG, FUSED, EARLY, ROUTED>), dim3(blocks, gy, gz),
+        hipLaunchKernelGGL((gemv_q4_0_q8_1_kernel<M, U, JS, RG, FUSED, EARLY, ROUTED>), dim3(blocks, gy),
                            dim3(64 * JS * RG), smem, stream, (const uint8_t *)w, xin, xq_out, y, K, N, ra);
     }
     return hipGetLastError();
@@ -922,26 +1023,31 @@ hipError_t launch_cfg(const void *w, const void *xin, uint8_t *xq_out, float *y,
 
 template <bool SPLIT, int M, int U, int JS, bool FUSED, bool ROUTED = false>
 hipError_t launch_js(const void *w, const void *xin, uint8_t *xq_out, float *y, int K, int N, hipStream_t stream,
-                     const RouteArgs &ra = RouteArgs{}, int gy = 1, int gz = 1) {
+                     const RouteArgs &ra = RouteArgs{}, int gy = 1) {
     constexpr int RG = rg_pick<SPLIT, M, JS, FUSED, ROUTED>();
     const int n_items = FUSED ? 2 * (K / kQK) : M * (K / kQK);
     const int rounds = (n_items + 64 * JS * RG - 1) / (64 * JS * RG);
-    if (rounds <= 1) return launch_cfg<SPLIT, M, U, JS, FUSED, 1, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy, gz);
-    if (rounds <= 2) return launch_cfg<SPLIT, M, U, JS, FUSED, 2, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy, gz);
-    return launch_cfg<SPLIT, M, U, JS, FUSED, 4, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy, gz);
+    // Routed block_q4_0 at 4 routes and four K slices: only the first round ahead of
+    // the weights (its chunk loop keeps the 36 raw weight dwords of four rows live;
+    // two early rounds spill at 1024 threads' 128 registers).
+    if constexpr (ROUTED && !SPLIT && M == 4 && JS == 4 && RG == 4)
+        return launch_cfg<SPLIT, M, U, JS, FUSED, 1, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy);
+    if (rounds <= 1) return launch_cfg<SPLIT, M, U, JS, FUSED, 1, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy);
+    if (rounds <= 2) return launch_cfg<SPLIT, M, U, JS, FUSED, 2, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy);
+    return launch_cfg<SPLIT, M, U, JS, FUSED, 4, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy);
 }
 
 template <bool SPLIT, int M, int U, bool FUSED, bool ROUTED = false>
 hipError_t launch_m(const void *w, const void *xin, uint8_t *xq_out, float *y, int K, int N, hipStream_t stream,
-                    const RouteArgs &ra = RouteArgs{}, int gy = 1, int gz = 1) {
+                    const RouteArgs &ra = RouteArgs{}, int gy = 1) {
     const int js = (K / 64 + 63) / 64;
     switch (js) {
-        case 1: return launch_js<SPLIT, M, U, 1, FUSED, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy, gz);
-        case 2: return launch_js<SPLIT, M, U, 2, FUSED, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy, gz);
+        case 1: return launch_js<SPLIT, M, U, 1, FUSED, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy);
+        case 2: return launch_js<SPLIT, M, U, 2, FUSED, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy);
         case 3:
             return launch_js<SPLIT, M, (SPLIT && M == 1 && !FUSED) ? 2 : U, 3, FUSED, ROUTED>(w, xin, xq_out, y, K, N,
-                                                                                           stream, ra, gy, gz);
-        case 4: return launch_js<SPLIT, M, U, 4, FUSED, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy, gz);
+                                                                                           stream, ra, gy);
+        case 4: return launch_js<SPLIT, M, U, 4, FUSED, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy);
         default: return hipErrorInvalidValue;  // K > 16384: the C ABI routes these to the MFMA GEMM
     }
 }
@@ -1012,18 +1118,17 @@ hipError_t launch_gemv_routed(const void *w, const void *w2, const void *xq, con
     const int slots = n_experts < n_routes ? n_experts : n_routes;
     const RouteArgs ra{expert_offsets, (const uint8_t *)w2, n_experts, n_routes, slots, ldy};
     const int gy = slots * (w2 != nullptr ? 2 : 1);
-    const int gz = (max_routes_per_expert + mt - 1) / mt;
     if (split) {
         switch (mt) {
-            case 1: return launch_m<true, 1, JJO_Q4S_U1, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy, gz);
-            case 2: return launch_m<true, 2, 2, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy, gz);
-            default: return launch_m<true, 4, 4, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy, gz);
+            case 1: return launch_m<true, 1, JJO_Q4S_U1, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
+            case 2: return launch_m<true, 2, 2, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
+            default: return launch_m<true, 4, 4, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
         }
     }
     switch (mt) {
-        case 1: return launch_m<false, 1, kU1, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy, gz);
-        case 2: return launch_m<false, 2, 2, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy, gz);
-        default: return launch_m<false, 4, kU4, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy, gz);
+        case 1: return launch_m<false, 1, kU1, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
+        case 2: return launch_m<false, 2, 2, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
+        default: return launch_m<false, 4, kU4, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
     }
 }
 

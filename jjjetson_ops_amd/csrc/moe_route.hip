@@ -162,37 +162,68 @@ __global__ __launch_bounds__(256) void moe_gather_q8_1_kernel(const uint8_t *__r
 
 // ---------------------------------------------------------------- decode routing
 // Decode batches (at most kMoeDecodeRoutes routes): quantize, top-k, dispatch and
-// gather in one launch.  Workgroup p (one per sorted route position) recomputes
-// the top-k of every token (top_k_token, the same bits as moe_top_k_kernel) and
-// the stable positions
+// gather in one launch.  Workgroup r owns route r = t * top_k + k: it issues the
+// loads of token t's fp32 row first, then recomputes the top-k of every token
+// (top_k_token over logits staged in LDS: the same bits as moe_top_k_kernel) and
+// the stable position of each route
 //   pos(r) = #{r' : e(r') < e(r)} + #{r' < r : e(r') = e(r)}
-// (moe_dispatch_kernel's order), then quantizes the fp32 row of its route's token
-// into Q8_1 row p of xp with the quantizer's group arithmetic (quantize_group8:
-// the bytes launch_quantize_q8_1 + moe_gather_q8_1 give).  Workgroup 0 also
-// writes the routing tables.
+// (moe_dispatch_kernel's order), and quantizes the row into Q8_1 row pos(r) of xp
+// with the quantizer's group arithmetic (quantize_group8: the bytes of
+// launch_quantize_q8_1 + moe_gather_q8_1).  Workgroup 0 also writes the tables.
+constexpr int kDecodeLogitsLds = 4096;  // logits staged in LDS up to this many
+constexpr int kDecodeRowRegs = 4;       // float4 per thread loaded up front (1024 threads' worth per step)
+
+__device__ __forceinline__ void quantize_store_q8_1(float4 v, int i0, uint8_t *__restrict__ xp, int R, int pos) {
+    uint32_t ds;
+    const uint32_t q = quantize_group8(v.x, v.y, v.z, v.w, &ds);
+    uint8_t *out = xp + ((size_t)(i0 / kQSuper) * R + pos) * kQ8BlockBytes;
+    const int iqs = i0 % kQSuper;
+    *reinterpret_cast<uint32_t *>(out + 16 + iqs) = q;
+    if ((iqs & 31) == 0) *reinterpret_cast<uint32_t *>(out + 4 * (iqs / 32)) = ds;
+}
+
 __global__ __launch_bounds__(256) void moe_route_decode_kernel(
     const float *__restrict__ x, const float *__restrict__ logits, int num_tokens, int hidden, int num_experts,
     int top_k, float *__restrict__ route_w, int *__restrict__ ids, int32_t *__restrict__ expert_offsets,
     int32_t *__restrict__ src_route, int32_t *__restrict__ dst_of_route, uint8_t *__restrict__ xp) {
     __shared__ int s_ids[kMoeDecodeRoutes];
     __shared__ float s_w[kMoeDecodeRoutes];
-    __shared__ int s_src[kMoeDecodeRoutes];
+    __shared__ int s_pos[kMoeDecodeRoutes];
+    __shared__ float s_logits[kDecodeLogitsLds];
     const int R = num_tokens * top_k;
+    const int r_own = blockIdx.x;
     const bool lead = blockIdx.x == 0;
-    for (int t = threadIdx.x; t < num_tokens; t += blockDim.x)
-        top_k_token(logits + (size_t)t * num_experts, num_experts, top_k, s_w + t * top_k, s_ids + t * top_k);
+    // 1) this route's token row: the first 1024 * kDecodeRowRegs values in flight now
+    //    (hidden % 128 == 0: every 32-lane half-wave is live or idle as a whole)
+    const float *row = x + (size_t)(r_own / top_k) * hidden;
+    float4 xv[kDecodeRowRegs];
+#pragma unroll
+    for (int i = 0; i < kDecodeRowRegs; ++i) {
+        const int i0 = (threadIdx.x + i * 256) * 4;
+        xv[i] = i0 < hidden ? *reinterpret_cast<const float4 *>(row + i0) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    // 2) top-k of every token
+    const int n_logits = num_tokens * num_experts;
+    const bool staged = n_logits <= kDecodeLogitsLds;
+    if (staged)
+        for (int i = threadIdx.x; i < n_logits; i += blockDim.x) s_logits[i] = logits[i];
     __syncthreads();
+    const float *lg = staged ? s_logits : logits;
+    for (int t = threadIdx.x; t < num_tokens; t += blockDim.x)
+        top_k_token(lg + (size_t)t * num_experts, num_experts, top_k, s_w + t * top_k, s_ids + t * top_k);
+    __syncthreads();
+    // 3) stable positions (ids clamped to a valid expert, as in moe_dispatch_kernel)
     for (int r = threadIdx.x; r < R; r += blockDim.x) {
-        // (ids clamped to a valid expert, as in moe_dispatch_kernel: memory safety)
         const int e = min(max(s_ids[r], 0), num_experts - 1);
         int pos = 0;
         for (int j = 0; j < R; ++j) {
             const int ej = min(max(s_ids[j], 0), num_experts - 1);
             pos += (ej < e) | ((ej == e) & (j < r));
         }
-        s_src[pos] = r;
+        s_pos[r] = pos;
         if (lead) {
             dst_of_route[r] = pos;
+            src_route[pos] = r;
             route_w[r] = s_w[r];
             ids[r] = s_ids[r];
         }
@@ -205,20 +236,15 @@ __global__ __launch_bounds__(256) void moe_route_decode_kernel(
         }
     }
     __syncthreads();
-    if (lead)
-        for (int r = threadIdx.x; r < R; r += blockDim.x) src_route[r] = s_src[r];
-    const int p = blockIdx.x;
-    const float *row = x + (size_t)(s_src[p] / top_k) * hidden;
-    // hidden % 128 == 0: every 32-lane half-wave is live or idle as a whole
-    for (int i0 = threadIdx.x * 4; i0 < hidden; i0 += blockDim.x * 4) {
-        const float4 v = *reinterpret_cast<const float4 *>(row + i0);
-        uint32_t ds;
-        const uint32_t q = quantize_group8(v.x, v.y, v.z, v.w, &ds);
-        uint8_t *out = xp + ((size_t)(i0 / kQSuper) * R + p) * kQ8BlockBytes;
-        const int iqs = i0 % kQSuper;
-        *reinterpret_cast<uint32_t *>(out + 16 + iqs) = q;
-        if ((iqs & 31) == 0) *reinterpret_cast<uint32_t *>(out + 4 * (iqs / 32)) = ds;
+    // 4) Q8_1 row pos(r_own) of xp
+    const int pos = s_pos[r_own];
+#pragma unroll
+    for (int i = 0; i < kDecodeRowRegs; ++i) {
+        const int i0 = (threadIdx.x + i * 256) * 4;
+        if (i0 < hidden) quantize_store_q8_1(xv[i], i0, xp, R, pos);
     }
+    for (int i0 = (threadIdx.x + kDecodeRowRegs * 256) * 4; i0 < hidden; i0 += 1024)
+        quantize_store_q8_1(*reinterpret_cast<const float4 *>(row + i0), i0, xp, R, pos);
 }
 
 // ---------------------------------------------------------------- combine

@@ -372,6 +372,30 @@ def test_moe_ffn_end_to_end(T, H, I, E, top_k, dev):
     np.testing.assert_allclose(y_ffn, ref, rtol=2e-3, atol=2e-3)
 
 
+@pytest.mark.parametrize("T,H,I,E,top_k", [(16, 256, 384, 8, 2), (9, 512, 256, 4, 1), (2, 256, 5120, 8, 2),
+                                            (16, 128, 128, 64, 8)])
+def test_moe_ffn_decode_skewed_routing(T, H, I, E, top_k, dev):
+    """Every token on the same top_k experts: each active expert holds T routes, so a
+    routed-GEMV workgroup takes them in several chunks (weights kept in registers)."""
+    import torch
+    note(f"moe_ffn skewed T={T} H={H} I={I} E={E} k={top_k}")
+    x, lg, wg, wu, wd = _ffn_inputs(T, H, I, E, 700 + T)
+    lg = lg.copy()
+    lg[:, :top_k] += 20.0
+    ref = _oracle_ffn(x, lg, wg, wu, wd, top_k)
+    d = {k: to_dev(v, dev) for k, v in dict(x=x, lg=lg, wg=np.concatenate(wg), wu=np.concatenate(wu),
+                                          wd=np.concatenate(wd)).items()}
+    ws = torch.empty(capi.moe_ffn_workspace_bytes(T, H, I, E, top_k), dtype=torch.uint8, device=dev)
+    for split in (False, True):
+        mats = [d["wg"], d["wu"], d["wd"]]
+        if split:
+            mats = [_split_stack(d["wg"], E * I, H, dev), _split_stack(d["wu"], E * I, H, dev),
+                    _split_stack(d["wd"], E * H, I, dev)]
+        y = torch.full((T * H,), float("nan"), dtype=torch.float32, device=dev)
+        capi.moe_ffn(d["x"], d["lg"], *mats, y, T, H, I, E, top_k, ws, split=split)
+        np.testing.assert_allclose(host(y).reshape(T, H), ref, rtol=2e-3, atol=2e-3)
+
+
 def test_moe_ffn_rejects_small_workspace(dev):
     import torch
     T, H, I, E, k = 4, 128, 128, 4, 2
