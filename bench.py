@@ -226,7 +226,8 @@ def time_moe_ffn(dev, steps, warmup, split=False, T=512):
     GEMVs).  Decode steps read only their active experts (2 x 99 MB at T=1), which
     the 256 MB MALL could keep between steps: there the step rotates over 4 router
     logit sets that pick different experts and 2 copies of the weights (1.6 GB per
-    cycle), as consecutive layers of a model would."""
+    cycle), as consecutive layers of a model would; from T=4 on every step routes
+    each token to its own pair of experts (all 8 active, T/4 routes each)."""
     import torch
     from jjjetson_ops_amd import capi
 
@@ -248,12 +249,16 @@ def time_moe_ffn(dev, steps, warmup, split=False, T=512):
     torch.cuda.synchronize()
     g = torch.Generator(device="cpu").manual_seed(4)
     if decode:
-        # logit set j favours experts 2j and 2j+1 for every token
+        # logit set j favours experts 2(j+t) and 2(j+t)+1 (mod 8) for token t: one
+        # token reads a different pair in each set; T >= 4 spreads over all 8 experts
         base = torch.randn(T, E, generator=g)
         logit_sets = []
         for j in range(4):
             lg = base.clone()
-            lg[:, 2 * j:2 * j + 2] += 8.0
+            for t in range(T):
+                e0 = (2 * (j + t)) % E
+                lg[t, e0] += 8.0
+                lg[t, e0 + 1] += 8.0
             logit_sets.append(lg)
     else:
         logit_sets = [torch.randn(T, E, generator=g)]

@@ -357,8 +357,10 @@ int moe_combine_device(void *stream, const float *expert_out, const int32_t *dst
  * The whole Q4_0 MoE FFN on device pointers: x fp32 [T][H], logits fp32 [T][E],
  * y fp32 [T][H].  `workspace` (256-byte aligned) holds every intermediate; its
  * size is moe_q4_0_ffn_workspace_bytes(...).  Seven launches (quantize x, top-k,
- * dispatch, gather, gate|up with SwiGLU and Q8_1, down, combine), no allocation,
- * asynchronous on `stream`.  H % 128 == 0, I % 128 == 0.
+ * dispatch, gather, gate|up with SwiGLU and Q8_1, down, combine); at 16 tokens or
+ * fewer (H, I <= 16384) five (routing in one launch, gate|up over the active experts
+ * into an fp32 [R][2I] part of the workspace, SwiGLU + Q8_1, down, combine).  No
+ * allocation, asynchronous on `stream`.  H % 128 == 0, I % 128 == 0.
  */
 int64_t moe_q4_0_ffn_workspace_bytes(int num_tokens, int hidden_size, int intermediate_size, int num_experts,
                                      int top_k);
@@ -368,7 +370,8 @@ int moe_q4_0_ffn_forward_device(void *stream, const float *x, const float *logit
                                 int64_t workspace_bytes);
 /* The same FFN on expert weights repacked into the split layout (each of gate, up
  * and down as one [E * rows] matrix, 16-byte aligned); y equals the block_q4_0
- * entry's bit for bit. */
+ * entry's bit for bit above 16 tokens (below, both are within fp32 rounding of the
+ * oracle: the two layouts' GEMVs sum a row in different orders). */
 int moe_q4_0s_ffn_forward_device(void *stream, const float *x, const float *logits, const void *w_gate_split,
                                  const void *w_up_split, const void *w_down_split, float *y, int num_tokens,
                                  int hidden_size, int intermediate_size, int num_experts, int top_k, void *workspace,

@@ -969,13 +969,18 @@ int moe_ffn_run(bool split, void *stream, const float *x, const float *logits, c
     const int R = T * top_k;
     hipError_t e;
     if (moe_decode_path(T, H, I, top_k)) {
-        // A token's top_k experts are distinct: no expert holds more than T routes.
+        // Chunk size of the routed GEMVs: the mean routes per active expert (an expert
+        // with more takes several chunks with its weights held in registers).
+#ifndef JJO_MOE_CHUNK_MEAN
+#define JJO_MOE_CHUNK_MEAN 1
+#endif
         // 1) quantize + top-k + dispatch + gather, 2) gate|up (both matrices, one
         // launch) -> fp32 [R][2I], 3) SwiGLU + Q8_1, 4) down projection, 5) combine
         if ((e = launch_moe_route_decode(x, logits, T, H, E, top_k, ws.route_w, ws.ids, ws.offsets, ws.src_route,
                                          ws.dst_of_route, ws.xp, s)) != hipSuccess)
             return hip_fail(e, "moe_ffn routing");
-        const int per_expert = T < R ? T : R;
+        const int active = E < R ? E : R;
+        const int per_expert = JJO_MOE_CHUNK_MEAN ? (R + active - 1) / active : (T < R ? T : R);
         if ((e = launch_gemv_routed(w_gate, w_up, ws.xp, ws.offsets, E, R, per_expert, ws.gate_up, 2 * I, H, I,
                                     split, s)) != hipSuccess)
             return hip_fail(e, "moe_ffn gate_up (routed GEMV)");
