@@ -396,6 +396,35 @@ def test_moe_ffn_decode_skewed_routing(T, H, I, E, top_k, dev):
         np.testing.assert_allclose(host(y).reshape(T, H), ref, rtol=2e-3, atol=2e-3)
 
 
+@pytest.mark.parametrize("T", [1, 3])
+def test_moe_ffn_decode_repeated_expert(T, dev):
+    """A token whose only finite logit is expert 0 selects expert 0 twice (the
+    reference's top-k rule: a taken expert reads -inf, and the first id wins a tie
+    of -inf), so expert 0 holds more routes than tokens: the routed GEMVs must take
+    every route (the second has weight 0 and must still be computed, not left as
+    whatever the workspace held)."""
+    import torch
+    H, I, E, k = 256, 384, 8, 2
+    note(f"moe_ffn repeated expert T={T}")
+    x, lg, wg, wu, wd = _ffn_inputs(T, H, I, E, 800 + T)
+    lg = lg.copy()
+    lg[0, 1:] = -np.inf
+    ids, _ = oracle_np.moe_top_k(lg, k)
+    assert list(ids[0]) == [0, 0]
+    ref = _oracle_ffn(x, lg, wg, wu, wd, k)
+    d = {n: to_dev(v, dev) for n, v in dict(x=x, lg=lg, wg=np.concatenate(wg), wu=np.concatenate(wu),
+                                          wd=np.concatenate(wd)).items()}
+    ws = torch.full((capi.moe_ffn_workspace_bytes(T, H, I, E, k),), 255, dtype=torch.uint8, device=dev)  # NaN fill
+    for split in (False, True):
+        mats = [d["wg"], d["wu"], d["wd"]]
+        if split:
+            mats = [_split_stack(d["wg"], E * I, H, dev), _split_stack(d["wu"], E * I, H, dev),
+                    _split_stack(d["wd"], E * H, I, dev)]
+        y = torch.full((T * H,), float("nan"), dtype=torch.float32, device=dev)
+        capi.moe_ffn(d["x"], d["lg"], *mats, y, T, H, I, E, k, ws, split=split)
+        np.testing.assert_allclose(host(y).reshape(T, H), ref, rtol=2e-3, atol=2e-3)
+
+
 def test_moe_ffn_rejects_small_workspace(dev):
     import torch
     T, H, I, E, k = 4, 128, 128, 4, 2
