@@ -516,6 +516,25 @@ int jjo_read_floor_device(const void *d_src, int64_t bytes, uint32_t *d_out, voi
     return e == hipSuccess ? JJO_OK : hip_fail(e, "read_floor launch");
 }
 
+}  // extern "C"
+
+namespace {
+// Grouped launches with few routes (decode batches) run as routed GEMVs over the
+// active experts: the 128-route MFMA tiles would leave most of the GPU idle.
+#ifndef JJO_GROUPED_GEMV_ROUTES
+#define JJO_GROUPED_GEMV_ROUTES 48
+#endif
+constexpr int kGroupedGemvRoutes = JJO_GROUPED_GEMV_ROUTES;
+bool grouped_gemv(int n_routes, int K) { return n_routes <= kGroupedGemvRoutes && K <= kGemvMaxK; }
+// Routes per active expert expected: the chunk size of the routed GEMV.
+int mean_routes(int n_routes, int n_experts) {
+    const int active = n_experts < n_routes ? n_experts : n_routes;
+    return (n_routes + active - 1) / active;
+}
+}  // namespace
+
+extern "C" {
+
 int mat_mul_q4_0_q8_1_grouped_device(const void *d_w_q4_0, const void *d_x_q8_1,
                                      const int32_t *d_expert_offsets, int n_experts,
                                      const int32_t *d_route_dst, float *d_y, int ncols_k,
@@ -527,8 +546,12 @@ int mat_mul_q4_0_q8_1_grouped_device(const void *d_w_q4_0, const void *d_x_q8_1,
         return set_error(JJO_ERR_INVALID_ARG, "expert_offsets must be non-null and 1 <= n_experts <= 4096");
     if ((rc = check_grouped_grid(n_routes, n_experts)) != JJO_OK) return rc;
     if ((rc = require_gfx950()) != JJO_OK) return rc;
-    hipError_t e = launch_gemm_mfma_grouped(d_w_q4_0, d_x_q8_1, d_expert_offsets, n_experts, d_route_dst,
-                                            d_y, ncols_k, nrows_out, n_routes, (hipStream_t)stream);
+    hipError_t e = grouped_gemv(n_routes, ncols_k)
+                       ? launch_gemv_routed(d_w_q4_0, nullptr, d_x_q8_1, d_expert_offsets, n_experts, n_routes,
+                                            mean_routes(n_routes, n_experts), d_y, nrows_out, ncols_k, nrows_out,
+                                            false, (hipStream_t)stream, d_route_dst)
+                       : launch_gemm_mfma_grouped(d_w_q4_0, d_x_q8_1, d_expert_offsets, n_experts, d_route_dst,
+                                                  d_y, ncols_k, nrows_out, n_routes, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "grouped gemm launch");
     return JJO_OK;
 }
@@ -544,9 +567,13 @@ int mat_mul_q4_0s_q8_1_grouped_device(const void *d_w_split, const void *d_x_q8_
         return set_error(JJO_ERR_INVALID_ARG, "expert_offsets must be non-null and 1 <= n_experts <= 4096");
     if ((rc = check_grouped_grid(n_routes, n_experts)) != JJO_OK) return rc;
     if ((rc = require_gfx950()) != JJO_OK) return rc;
-    hipError_t e = launch_gemm_mfma_grouped(d_w_split, d_x_q8_1, d_expert_offsets, n_experts, d_route_dst,
-                                            d_y, ncols_k, nrows_out, n_routes, (hipStream_t)stream, nullptr, 0,
-                                            true);
+    hipError_t e = grouped_gemv(n_routes, ncols_k)
+                       ? launch_gemv_routed(d_w_split, nullptr, d_x_q8_1, d_expert_offsets, n_experts, n_routes,
+                                            mean_routes(n_routes, n_experts), d_y, nrows_out, ncols_k, nrows_out,
+                                            true, (hipStream_t)stream, d_route_dst)
+                       : launch_gemm_mfma_grouped(d_w_split, d_x_q8_1, d_expert_offsets, n_experts, d_route_dst,
+                                                  d_y, ncols_k, nrows_out, n_routes, (hipStream_t)stream, nullptr,
+                                                  0, true);
     if (e != hipSuccess) return hip_fail(e, "grouped gemm (split layout) launch");
     return JJO_OK;
 }
@@ -895,9 +922,14 @@ int moe_q4_0_gate_up_device(void *stream, const void *w_gate, const void *w_up, 
         return set_error(JJO_ERR_INVALID_ARG, "moe_gate_up: intermediate_size must be a multiple of 128");
     if ((rc = check_grouped_grid(n_routes, num_experts)) != JJO_OK) return rc;
     if ((rc = require_gfx950()) != JJO_OK) return rc;
-    hipError_t e = launch_gemm_mfma_grouped(w_gate, x_q8_1_permuted, expert_offsets, num_experts, nullptr, gate_up,
-                                            hidden_size, 2 * intermediate_size, n_routes, (hipStream_t)stream, w_up,
-                                            intermediate_size);
+    hipError_t e =
+        grouped_gemv(n_routes, hidden_size)
+            ? launch_gemv_routed(w_gate, w_up, x_q8_1_permuted, expert_offsets, num_experts, n_routes,
+                                 mean_routes(n_routes, num_experts), gate_up, 2 * intermediate_size, hidden_size,
+                                 intermediate_size, false, (hipStream_t)stream)
+            : launch_gemm_mfma_grouped(w_gate, x_q8_1_permuted, expert_offsets, num_experts, nullptr, gate_up,
+                                       hidden_size, 2 * intermediate_size, n_routes, (hipStream_t)stream, w_up,
+                                       intermediate_size);
     return e == hipSuccess ? JJO_OK : hip_fail(e, "moe_gate_up launch");
 }
 
@@ -971,16 +1003,12 @@ int moe_ffn_run(bool split, void *stream, const float *x, const float *logits, c
     if (moe_decode_path(T, H, I, top_k)) {
         // Chunk size of the routed GEMVs: the mean routes per active expert (an expert
         // with more takes several chunks with its weights held in registers).
-#ifndef JJO_MOE_CHUNK_MEAN
-#define JJO_MOE_CHUNK_MEAN 1
-#endif
         // 1) quantize + top-k + dispatch + gather, 2) gate|up (both matrices, one
         // launch) -> fp32 [R][2I], 3) SwiGLU + Q8_1, 4) down projection, 5) combine
         if ((e = launch_moe_route_decode(x, logits, T, H, E, top_k, ws.route_w, ws.ids, ws.offsets, ws.src_route,
                                          ws.dst_of_route, ws.xp, s)) != hipSuccess)
             return hip_fail(e, "moe_ffn routing");
-        const int active = E < R ? E : R;
-        const int per_expert = JJO_MOE_CHUNK_MEAN ? (R + active - 1) / active : (T < R ? T : R);
+        const int per_expert = mean_routes(R, E);
         if ((e = launch_gemv_routed(w_gate, w_up, ws.xp, ws.offsets, E, R, per_expert, ws.gate_up, 2 * I, H, I,
                                     split, s)) != hipSuccess)
             return hip_fail(e, "moe_ffn gate_up (routed GEMV)");

@@ -291,12 +291,17 @@ __device__ __forceinline__ void finish_f32(uint8_t *xs, uint8_t *__restrict__ xq
 // keeps its weight rows in registers and takes the expert's routes M at a time
 // (each chunk re-stages only activation rows), so every weight byte of an active
 // expert is read once whatever its route count.  Output row p (a sorted route
-// position) starts at y + p * ldy.
+// position) starts at y + p * ldy, or at y + route_dst[p] * ldy.
 struct RouteArgs {
-    const int32_t *offsets;  // [n_experts + 1]
-    const uint8_t *w2;       // second stacked matrix, or null
+    const int32_t *offsets;    // [n_experts + 1]
+    const uint8_t *w2;         // second stacked matrix, or null
+    const int32_t *route_dst;  // output row of sorted route p (null: p)
     int n_experts, n_routes, slots, ldy;
 };
+
+__device__ __forceinline__ size_t routed_row(const RouteArgs &ra, int p) {
+    return ra.route_dst != nullptr ? (size_t)ra.route_dst[p] : (size_t)p;
+}
 
 struct RouteTile {
     int expert, which, m0, mc, end;  // first chunk: routes m0 .. m0 + mc - 1; the expert's end
@@ -397,7 +402,7 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
     if constexpr (ROUTED) {
         if (!route_tile(ra, M, rt)) return;
         w = (rt.which ? ra.w2 : w) + (size_t)rt.expert * N * row_bytes;
-        y += (size_t)rt.m0 * ra.ldy + (size_t)rt.which * N;
+        y += (size_t)rt.which * N;
     }
     const int ldy = ROUTED ? ra.ldy : N;
     int m0c = rt.m0, mcc = rt.mc;  // the current chunk of routes (routed launches)
@@ -578,7 +583,7 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
         const int u = idx / M, m = idx % M;
         const bool owner = (lane & (64 / NV - 1)) == 0 && idx < U * M;
         if constexpr (JS == 1) {
-            if (owner && r0 + u < N) if (m < mcc) y[(size_t)m * ldy + r0 + u] = s;
+            if (owner && r0 + u < N && m < mcc) y[(ROUTED ? routed_row(ra, m0c + m) : (size_t)m) * ldy + r0 + u] = s;
         } else {
             if (owner) part[((rg * U + u) * M + m) * JS + js] = s;
             __syncthreads();
@@ -592,7 +597,7 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
                             float s = pp[0];
 #pragma unroll
                             for (int j = 1; j < JS; ++j) s += pp[j];
-                            if (m < mcc) y[(size_t)m * ldy + r0 + u] = s;
+                            if (m < mcc) y[(ROUTED ? routed_row(ra, m0c + m) : (size_t)m) * ldy + r0 + u] = s;
                         }
                     }
             }
@@ -604,7 +609,6 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
             m0c += M;
             if (m0c >= rt.end) break;
             mcc = min(M, rt.end - m0c);
-            y += (size_t)M * ldy;
             again = true;
             __syncthreads();  // every wave is done with the records and partial sums
             if constexpr (M <= 2) {
@@ -738,7 +742,7 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
         if (rt.which) w = ra.w2;
         plane_rows = (size_t)ra.n_experts * N;
         row0 = (size_t)rt.expert * N;
-        y += (size_t)rt.m0 * ra.ldy + (size_t)rt.which * N;
+        y += (size_t)rt.which * N;
     }
     const int ldy = ROUTED ? ra.ldy : N;
     int m0c = rt.m0, mcc = rt.mc;  // the current chunk of routes (routed launches)
@@ -892,7 +896,7 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
         const int u = idx / M, m = idx % M;
         const bool owner = (lane & (64 / NV - 1)) == 0 && idx < U * M;
         if constexpr (JS == 1) {
-            if (owner && r0 + u < N) if (m < mcc) y[(size_t)m * ldy + r0 + u] = s;
+            if (owner && r0 + u < N && m < mcc) y[(ROUTED ? routed_row(ra, m0c + m) : (size_t)m) * ldy + r0 + u] = s;
         } else {
             if (owner) part[((rg * U + u) * M + m) * JS + js] = s;
             __syncthreads();
@@ -906,7 +910,7 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
                             float s = pp[0];
 #pragma unroll
                             for (int j = 1; j < JS; ++j) s += pp[j];
-                            if (m < mcc) y[(size_t)m * ldy + r0 + u] = s;
+                            if (m < mcc) y[(ROUTED ? routed_row(ra, m0c + m) : (size_t)m) * ldy + r0 + u] = s;
                         }
                     }
             }
@@ -918,7 +922,6 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
             m0c += M;
             if (m0c >= rt.end) break;
             mcc = min(M, rt.end - m0c);
-            y += (size_t)M * ldy;
             again = true;
             __syncthreads();  // every wave is done with the records and partial sums
             if constexpr (M <= 2) {  // (as in gemv_q4_0_q8_1_kernel)
@@ -1112,11 +1115,11 @@ int gemv_routed_chunk(int max_routes_per_expert, int K, bool split) {
 
 hipError_t launch_gemv_routed(const void *w, const void *w2, const void *xq, const int32_t *expert_offsets,
                               int n_experts, int n_routes, int max_routes_per_expert, float *y, int ldy, int K, int N,
-                              bool split, hipStream_t stream) {
+                              bool split, hipStream_t stream, const int32_t *route_dst) {
     if (K > 16384 || max_routes_per_expert < 1) return hipErrorInvalidValue;
     const int mt = gemv_routed_chunk(max_routes_per_expert, K, split);
     const int slots = n_experts < n_routes ? n_experts : n_routes;
-    const RouteArgs ra{expert_offsets, (const uint8_t *)w2, n_experts, n_routes, slots, ldy};
+    const RouteArgs ra{expert_offsets, (const uint8_t *)w2, route_dst, n_experts, n_routes, slots, ldy};
     const int gy = slots * (w2 != nullptr ? 2 : 1);
     if (split) {
         switch (mt) {

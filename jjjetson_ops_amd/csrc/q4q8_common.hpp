@@ -54,13 +54,14 @@ hipError_t launch_gemv_q4s_fused(const void *w, const float *x, void *xq_out, fl
 // Routed GEMV over E stacked [N][K] experts (MoE decode): routes sorted by expert,
 // expert_offsets[E+1], Q8_1 route rows superblock-major over n_routes rows; each
 // active expert's weights are read once, its routes taken in chunks sized for
-// max_routes_per_expert (a bound the caller knows, e.g. the token count).  Sorted route p's output row
-// starts at y + p * ldy.  w2 (nullable): a second stacked matrix of the same shape,
+// max_routes_per_expert (routes per active expert expected; more take more chunks).
+// Sorted route p's output row starts at y + p * ldy, or at y + route_dst[p] * ldy
+// (route_dst nullable, entries unchecked).  w2 (nullable): a second stacked matrix of the same shape,
 // computed in the same launch into columns N..2N-1 of each output row.  K <= 16384;
 // split: both matrices in the split layout (planes over all E * N rows).
 hipError_t launch_gemv_routed(const void *w, const void *w2, const void *xq, const int32_t *expert_offsets,
                               int n_experts, int n_routes, int max_routes_per_expert, float *y, int ldy, int K, int N,
-                              bool split, hipStream_t stream);
+                              bool split, hipStream_t stream, const int32_t *route_dst = nullptr);
 // Routes per chunk of launch_gemv_routed (1, 2 or 4): its LDS holds that many
 // activation rows of K values (48 B per 32 values split, 40 B block_q4_0).
 int gemv_routed_chunk(int max_routes_per_expert, int K, bool split);

@@ -238,13 +238,31 @@ def test_moe_gate_up(T, H, I, E, top_k, dev):
                                    atol=ATOL)
 
 
+def _q8_1_scales(buf, rows, K):
+    """Per-value scale d of a superblock-major Q8_1 buffer of `rows` rows of K values."""
+    blk = buf.reshape(K // 128, rows, 144)
+    d = blk[:, :, :16].copy().view(np.float16).astype(np.float32)[:, :, 0::2]  # [K/128, rows, 4]
+    return np.repeat(d.transpose(1, 0, 2).reshape(rows, K // 32), 32, axis=1)
+
+
+def _dequant_q8_1(buf, rows, K):
+    blk = buf.reshape(K // 128, rows, 144)
+    q = blk[:, :, 16:].view(np.int8).astype(np.float32)  # [K/128, rows, 128]
+    return q.transpose(1, 0, 2).reshape(rows, K) * _q8_1_scales(buf, rows, K)
+
+
+GROUPED_GEMV_ROUTES = 48  # the grouped entries run routed GEMVs up to this many routes
+
+
 @pytest.mark.parametrize("T,H,I,E,top_k", MOE_CASES + [(3, 256, 256, 2, 2), (200, 128, 128, 2, 1),
                                                      (160, 256, 128, 1, 1), (330, 128, 256, 2, 1)])
 def test_moe_gate_up_swiglu_fused(T, H, I, E, top_k, dev):
     """The fused gate|up + SwiGLU + Q8_1 launch writes exactly the bytes of the
     unfused chain (grouped gate|up GEMM into fp32, then the SwiGLU quantizer); the
     cases cover experts of <= 8, <= 32, 160 (five column tiles in one chunk) and
-    about 165 routes (two chunks), and experts with no routes."""
+    about 165 routes (two chunks), and experts with no routes.  At 48 routes or fewer
+    the unfused gate|up runs as a routed GEMV (another summation order), so there
+    each value may sit one quantization step away."""
     import torch
     note(f"moe_gate_up_swiglu T={T} H={H} I={I} E={E} k={top_k}")
     rng = np.random.default_rng(500 + T)
@@ -262,7 +280,12 @@ def test_moe_gate_up_swiglu_fused(T, H, I, E, top_k, dev):
     capi.swiglu_quantize(gu, mq_ref, R, I)
     mq = torch.full((R * I // 128 * 144,), 0xA5, dtype=torch.uint8, device=dev)
     capi.moe_gate_up_swiglu(wg, wu, xp, off_d, E, mq, H, I, R)
-    assert np.array_equal(host(mq), host(mq_ref))
+    if R > GROUPED_GEMV_ROUTES:
+        assert np.array_equal(host(mq), host(mq_ref))
+    else:
+        a, b = _dequant_q8_1(host(mq), R, I), _dequant_q8_1(host(mq_ref), R, I)
+        step = np.maximum(_q8_1_scales(host(mq), R, I), _q8_1_scales(host(mq_ref), R, I))
+        assert (np.abs(a - b) <= step * 1.2).all()  # one step, and the fp16 scale's own rounding
 
 
 @pytest.mark.parametrize("rows,I", [(64, 384), (5, 128), (300, 256)])
@@ -445,22 +468,27 @@ def _split_stack(w_dev, rows, K, dev):
     return out
 
 
-@pytest.mark.parametrize("counts,N", [([1, 129, 0, 31, 160, 32, 33, 7], 256), ([3, 2, 1, 4], 384),
-                                      ([200, 0, 5], 300)])
-def test_grouped_split_layout(counts, N, dev):
+@pytest.mark.parametrize("counts,N,K", [([1, 129, 0, 31, 160, 32, 33, 7], 256, 512), ([3, 2, 1, 4], 384, 512),
+                                        ([200, 0, 5], 300, 512), ([0, 7, 0, 1], 100, 512), ([32], 256, 512),
+                                        ([2, 0, 9, 1], 256, 5120), ([5, 1], 96, 14336)])
+def test_grouped_split_layout(counts, N, K, dev):
     """The grouped GEMM on split-layout experts equals the block_q4_0 launch bit for
-    bit (the same kernel and arithmetic; only the weight loads differ), with route
-    scatter, empty experts, narrow and paired tails and a ragged N."""
+    bit above 48 routes (the same MFMA kernel; only the weight loads differ), with route
+    scatter, empty experts, narrow and paired tails and a ragged N.  At 48 routes or
+    fewer both run as routed GEMVs, whose two layouts sum a row in different orders:
+    both are checked against the oracle, scattered through route_dst."""
     import torch
-    E, K = len(counts), 512
-    note(f"grouped split counts={counts} N={N}")
+    E = len(counts)
+    note(f"grouped split counts={counts} N={N} K={K}")
     offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
     R = int(offsets[-1])
     rng = np.random.default_rng(R + N)
     xq = c_oracle.quantize_q8_1(rng.standard_normal((R, K)).astype(np.float32), [K, R])
-    w = to_dev(np.concatenate([make_w(N, K, rng) for _ in range(E)]), dev)
+    w_h = [make_w(N, K, rng) for _ in range(E)]
+    w = to_dev(np.concatenate(w_h), dev)
     ws = _split_stack(w, E * N, K, dev)
-    dst = to_dev(rng.permutation(R).astype(np.int32), dev)
+    perm = rng.permutation(R).astype(np.int32)
+    dst = to_dev(perm, dev)
     off_d, xq_d = to_dev(offsets, dev), to_dev(xq, dev)
     y1 = torch.full((R * N,), float("nan"), dtype=torch.float32, device=dev)
     y2 = torch.full((R * N,), float("nan"), dtype=torch.float32, device=dev)
@@ -468,7 +496,17 @@ def test_grouped_split_layout(counts, N, dev):
     capi.grouped_mat_mul(ws, xq_d, off_d, y2, K, N, R, route_dst=dst, split=True)
     a, b = host(y1), host(y2)
     assert not np.isnan(a).any()
-    assert np.array_equal(a, b)
+    if R > GROUPED_GEMV_ROUTES:
+        assert np.array_equal(a, b)
+    else:
+        ref = np.zeros((R, N), dtype=np.float32)
+        blocks = xq.reshape(K // 128, R, 144)
+        for e in range(E):
+            if counts[e]:
+                ref[perm[offsets[e]:offsets[e + 1]]] = c_oracle.matmul(w_h[e], expert_slice(blocks, offsets, e), K,
+                                                                       N, counts[e])
+        np.testing.assert_allclose(a.reshape(R, N), ref, rtol=RTOL, atol=ATOL)
+        np.testing.assert_allclose(b.reshape(R, N), ref, rtol=RTOL, atol=ATOL)
 
 
 @pytest.mark.parametrize("T,H,I,E,top_k", MOE_CASES + MOE_DECODE_CASES)
