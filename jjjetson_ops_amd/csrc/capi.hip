@@ -820,16 +820,15 @@ struct MoeWs {
     int64_t bytes;
 };
 
-// Token counts up to which the FFN runs its expert matrices as routed GEMVs (one
-// workgroup row range per active expert, every weight byte of an active expert
-// read once per chunk of its routes) instead of 128-row MFMA tiles, which leave
-// most of the GPU idle when each expert holds a handful of routes.
+// Token counts up to which the FFN runs its expert matrices as routed GEMVs (every
+// weight byte of an active expert read once, its routes taken in chunks) instead of
+// 128-route MFMA tiles, which leave most of the GPU idle when each expert holds a
+// handful of routes.  Measured against the MFMA path on 8, 64 and 256 experts (top-2,
+// top-8, top-8): the GEMVs win up to 16 tokens on all three and lose from 24-32 on.
 #ifndef JJO_MOE_GEMV_TOKENS
 #define JJO_MOE_GEMV_TOKENS 16
 #endif
-bool moe_decode_path(int T, int H, int I, int top_k) {
-    return T <= JJO_MOE_GEMV_TOKENS && T * top_k <= kMoeDecodeRoutes && H <= 16384 && I <= 16384;
-}
+bool moe_decode_path(int T, int H, int I) { return T <= JJO_MOE_GEMV_TOKENS && H <= 16384 && I <= 16384; }
 
 // Workspace carve-up, every part 256-byte aligned.
 MoeWs moe_ws_layout(uint8_t *base, int T, int H, int I, int E, int top_k) {
@@ -850,7 +849,7 @@ MoeWs moe_ws_layout(uint8_t *base, int T, int H, int I, int E, int top_k) {
     w.xp = take(R * (H / kQSuper) * kQ8BlockBytes);
     w.midq = take(R * (I / kQSuper) * kQ8BlockBytes);
     w.eout = (float *)take(R * H * 4);
-    w.gate_up = moe_decode_path(T, H, I, top_k) ? (float *)take(R * 2 * I * 4) : nullptr;
+    w.gate_up = moe_decode_path(T, H, I) ? (float *)take(R * 2 * I * 4) : nullptr;
     w.bytes = off;
     return w;
 }
@@ -1000,14 +999,24 @@ int moe_ffn_run(bool split, void *stream, const float *x, const float *logits, c
     hipStream_t s = (hipStream_t)stream;
     const int R = T * top_k;
     hipError_t e;
-    if (moe_decode_path(T, H, I, top_k)) {
+    if (moe_decode_path(T, H, I)) {
         // Chunk size of the routed GEMVs: the mean routes per active expert (an expert
         // with more takes several chunks with its weights held in registers).
         // 1) quantize + top-k + dispatch + gather, 2) gate|up (both matrices, one
         // launch) -> fp32 [R][2I], 3) SwiGLU + Q8_1, 4) down projection, 5) combine
-        if ((e = launch_moe_route_decode(x, logits, T, H, E, top_k, ws.route_w, ws.ids, ws.offsets, ws.src_route,
-                                         ws.dst_of_route, ws.xp, s)) != hipSuccess)
-            return hip_fail(e, "moe_ffn routing");
+        if (R <= kMoeDecodeRoutes) {
+            if ((e = launch_moe_route_decode(x, logits, T, H, E, top_k, ws.route_w, ws.ids, ws.offsets,
+                                             ws.src_route, ws.dst_of_route, ws.xp, s)) != hipSuccess)
+                return hip_fail(e, "moe_ffn routing");
+        } else {  // more routes (top_k > 24) than the one-launch routing holds: four launches
+            if ((e = launch_quantize_q8_1(x, ws.xq, H, T, 1, s)) != hipSuccess) return hip_fail(e, "moe_ffn quantize x");
+            if ((e = launch_moe_top_k(logits, ws.route_w, ws.ids, T, E, top_k, s)) != hipSuccess)
+                return hip_fail(e, "moe_ffn top_k");
+            if ((e = launch_moe_dispatch(ws.ids, R, E, ws.offsets, ws.src_route, ws.dst_of_route, s)) != hipSuccess)
+                return hip_fail(e, "moe_ffn dispatch");
+            if ((e = launch_moe_gather_q8_1(ws.xq, ws.src_route, ws.xp, T, R, top_k, H, s)) != hipSuccess)
+                return hip_fail(e, "moe_ffn gather");
+        }
         const int per_expert = mean_routes(R, E);
         if ((e = launch_gemv_routed(w_gate, w_up, ws.xp, ws.offsets, E, R, per_expert, ws.gate_up, 2 * I, H, I,
                                     split, s)) != hipSuccess)

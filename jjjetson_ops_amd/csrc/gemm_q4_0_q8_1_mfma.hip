@@ -108,24 +108,42 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_q4_0_q8_1_mfma_kernel(
         // than 32 tokens (expert by expert), then every short tail tile (at most 32
         // tokens, run narrow below).  The long tiles thus start in the first rounds of
         // the grid and the short ones fill its ragged end.
+        // Searched 64 experts per step: lane i takes expert e0 + i, a lane prefix sum of
+        // the tile counts and a ballot find the expert that holds tile t (the same
+        // enumeration as a walk over the experts, in O(E / 64) steps).
         int t = blockIdx.y;
         int e = 0;
         m0 = -1;
         m_end = 0;
         for (int pass = 0; pass < 2 && m0 < 0; ++pass) {
-            for (e = 0; e < n_experts; ++e) {
-                // Clamped to [0, M] and to beg <= end: a malformed table yields fewer
-                // tiles, never an access outside the activation and output buffers.
-                const int beg = min(max(expert_offsets[e], 0), M);
-                const int end = min(max(expert_offsets[e + 1], beg), M);
-                const int full = (end - beg) / BM, rem = (end - beg) % BM;
-                const int tiles = pass == 0 ? full + (rem > 32) : (rem > 0 && rem <= 32);
-                if (t < tiles) {
-                    m0 = beg + (pass == 0 ? t : full) * BM;
-                    m_end = end;
-                    break;
+            for (int e0 = 0; e0 < n_experts && m0 < 0; e0 += 64) {
+                const int ei = e0 + lane;
+                int beg = 0, end = 0, full = 0, tiles = 0;
+                if (ei < n_experts) {
+                    // Clamped to [0, M] and to beg <= end: a malformed table yields fewer
+                    // tiles, never an access outside the activation and output buffers.
+                    beg = min(max(expert_offsets[ei], 0), M);
+                    end = min(max(expert_offsets[ei + 1], beg), M);
+                    full = (end - beg) / BM;
+                    const int rem = (end - beg) % BM;
+                    tiles = pass == 0 ? full + (rem > 32) : (rem > 0 && rem <= 32);
                 }
-                t -= tiles;
+                int incl = tiles;
+#pragma unroll
+                for (int d = 1; d < 64; d <<= 1) {
+                    const int o = __shfl_up(incl, d);
+                    if (lane >= d) incl += o;
+                }
+                const int total = __shfl(incl, 63);
+                if (t < total) {
+                    const int f = __builtin_ctzll(__ballot(incl > t));  // the expert holding tile t
+                    const int tf = t - (__shfl(incl, f) - __shfl(tiles, f));
+                    m0 = __shfl(beg, f) + (pass == 0 ? tf : __shfl(full, f)) * BM;
+                    m_end = __shfl(end, f);
+                    e = e0 + f;
+                } else {
+                    t -= total;
+                }
             }
         }
         if (m0 < 0) return;  // uniform over the workgroup

@@ -17,65 +17,97 @@ namespace jjo {
 namespace {
 
 // ---------------------------------------------------------------- top-k
-// One lane per token (num_experts <= 1024, top_k <= 32).
-// Selection: moe_top_k.cu:120-176 -- top_k rounds, each takes the largest
-// remaining logit, the smaller expert id on ties; ids[k] in selection order.
+// One wave per token (num_experts <= 1024, top_k <= 32).
+// Selection: moe_top_k.cu:120-176 -- top_k rounds; round k scans e = 0..E-1 with
+// v(e) = -inf for an expert taken in an earlier round, else the logit, keeps e = 0's
+// value first and takes a later e only when strictly greater; ids[k] in selection
+// order.  That keeps the smallest id of the largest non-NaN value, or expert 0 when
+// v(0) is NaN (nothing compares greater than NaN), and it re-selects a taken expert
+// once only -inf values are left; the wave computes exactly that: each lane holds
+// experts lane + 64j in registers with a taken bit each, and a lane-local best
+// (value, id) over its non-NaN values is reduced over the wave (larger value, then
+// smaller id).
 // Weights: softmax over the selected logits (delayed_softmax, moe_top_k.cu:12-55,
 // 190-195): max = the first selected value, e_i = expf(v_i - max), and the sum is
 // the 32-lane xor butterfly of warp_reduce_xor_sum (include/cuda_utils.cuh:37-43)
-// over e_0..e_{top_k-1} placed in lanes 0..top_k-1 (zeros elsewhere), so the
-// association order is the reference's; w_i = e_i * (1 / sum).
-// One token: writes its top_k ids and weights (selection order) to ids[0..top_k)
-// and weights[0..top_k).
+// over e_0..e_{top_k-1} held by lanes 0..top_k-1 (zeros elsewhere), run on the
+// lanes themselves, so the association order is the reference's; w_i = e_i * (1 / sum).
+constexpr int kTopKPerLane = 16;  // 1024 experts / 64 lanes
+
+// All 64 lanes of the wave call this for one token; lanes 0..top_k-1 write
+// weights[lane] and ids[lane].
 __device__ __forceinline__ void top_k_token(const float *__restrict__ row, int num_experts, int top_k,
-                                            float *__restrict__ weights, int *__restrict__ ids) {
-    float sel[32];
-    int sel_id[32];
+                                            float *__restrict__ weights, int *__restrict__ ids, int lane) {
+    float v[kTopKPerLane];
+#pragma unroll
+    for (int j = 0; j < kTopKPerLane; ++j) {
+        const int e = lane + 64 * j;
+        v[j] = e < num_experts ? row[e] : 0.0f;
+    }
+    const float v0 = __shfl(v[0], 0);  // expert 0's logit
+    uint32_t taken = 0;                // bit j: expert lane + 64j
+    bool taken0 = false;
+    float my_v = 0.0f, mx = 0.0f;
+    int my_id = 0;
     for (int k = 0; k < top_k; ++k) {
-        float best = -INFINITY;
-        int best_id = -1;
-        for (int e = 0; e < num_experts; ++e) {
-            bool taken = false;
-            for (int j = 0; j < k; ++j) taken |= (sel_id[j] == e);
-            const float v = taken ? -INFINITY : row[e];
-            if (best_id < 0 || v > best) {  // strict: the first (smallest) id wins ties
-                best = v;
-                best_id = e;
+        float bv = -INFINITY;
+        int bid = 0x7fffffff;
+        bool ok = false;
+#pragma unroll
+        for (int j = 0; j < kTopKPerLane; ++j) {
+            const int e = lane + 64 * j;
+            const float x = ((taken >> j) & 1u) ? -INFINITY : v[j];
+            if (e < num_experts && x == x && (!ok || x > bv)) {  // ids ascend with j
+                bv = x;
+                bid = e;
+                ok = true;
             }
         }
-        sel[k] = best;
-        sel_id[k] = best_id;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv, off);
+            const int oid = __shfl_xor(bid, off);
+            const bool ook = __shfl_xor((int)ok, off) != 0;
+            if (ook && (!ok || ov > bv || (ov == bv && oid < bid))) {
+                bv = ov;
+                bid = oid;
+                ok = true;
+            }
+        }
+        const float v0k = taken0 ? -INFINITY : v0;
+        if (v0k != v0k) {  // v(0) NaN: the scan never leaves expert 0
+            bv = v0k;
+            bid = 0;
+        }
+        if (lane == (bid & 63)) taken |= 1u << (bid >> 6);
+        taken0 |= bid == 0;
+        if (k == 0) mx = bv;
+        if (lane == k) {
+            my_v = bv;
+            my_id = bid;
+        }
     }
-    float lanes[32];
+    const float ex = lane < top_k ? expf(my_v - mx) : 0.0f;
+    float t = ex;
 #pragma unroll
-    for (int l = 0; l < 32; ++l) lanes[l] = 0.0f;
-    const float mx = sel[0];
-    for (int k = 0; k < top_k; ++k) lanes[k] = expf(sel[k] - mx);
-    float tree[32];
-#pragma unroll
-    for (int l = 0; l < 32; ++l) tree[l] = lanes[l];
-#pragma unroll
-    for (int off = 16; off > 0; off >>= 1) {
-        float nx[32];
-#pragma unroll
-        for (int l = 0; l < 32; ++l) nx[l] = tree[l] + tree[l ^ off];
-#pragma unroll
-        for (int l = 0; l < 32; ++l) tree[l] = nx[l];
-    }
-    const float inv_sum = 1.0f / tree[0];
-    for (int k = 0; k < top_k; ++k) {
-        weights[k] = lanes[k] * inv_sum;
-        ids[k] = sel_id[k];
+    for (int off = 16; off > 0; off >>= 1) t = t + __shfl_xor(t, off);
+    const float inv_sum = 1.0f / __shfl(t, 0);
+    if (lane < top_k) {
+        weights[lane] = ex * inv_sum;
+        ids[lane] = my_id;
     }
 }
 
-__global__ __launch_bounds__(64) void moe_top_k_kernel(const float *__restrict__ logits,
-                                                       float *__restrict__ weights, int *__restrict__ ids,
-                                                       int num_tokens, int num_experts, int top_k) {
-    const int t = blockIdx.x * 64 + threadIdx.x;
-    if (t >= num_tokens) return;
+constexpr int kTopKWaves = 4;  // tokens per workgroup
+
+__global__ __launch_bounds__(64 * kTopKWaves) void moe_top_k_kernel(const float *__restrict__ logits,
+                                                                    float *__restrict__ weights,
+                                                                    int *__restrict__ ids, int num_tokens,
+                                                                    int num_experts, int top_k) {
+    const int t = blockIdx.x * kTopKWaves + (threadIdx.x >> 6);
+    if (t >= num_tokens) return;  // whole waves
     top_k_token(logits + (size_t)t * num_experts, num_experts, top_k, weights + (size_t)t * top_k,
-                ids + (size_t)t * top_k);
+                ids + (size_t)t * top_k, threadIdx.x & 63);
 }
 
 // ---------------------------------------------------------------- dispatch
@@ -105,18 +137,33 @@ __global__ __launch_bounds__(64 * kDispatchWaves) void moe_dispatch_kernel(
     // (out-of-range ids are clamped to a valid expert: memory safety, not semantics)
     for (int r = r_beg + lane; r < r_end; r += 64) atomicAdd(&my[min(max(ids[r], 0), num_experts - 1)], 1);
     __syncthreads();
-    // exclusive scan over (expert, wave): base of wave w for expert e
-    if (threadIdx.x == 0) {
-        int run = 0;
-        for (int e = 0; e < num_experts; ++e) {
-            expert_offsets[e] = run;
-            for (int w = 0; w < kDispatchWaves; ++w) {
-                const int c = cnt[w * num_experts + e];
-                cnt[w * num_experts + e] = run;
-                run += c;
-            }
+    // exclusive scan over (expert, wave): base of wave w for expert e.  Thread e
+    // (num_experts <= 1024 = the workgroup) totals its expert's wave counts; a scan
+    // of those totals (within each wave, then over the waves' sums) gives the
+    // expert's base, then its waves' bases follow in wave order.
+    __shared__ int wave_sum[kDispatchWaves];
+    const int e_own = threadIdx.x;
+    int tot = 0;
+    if (e_own < num_experts)
+        for (int w = 0; w < kDispatchWaves; ++w) tot += cnt[w * num_experts + e_own];
+    int incl = tot;  // inclusive scan within the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int o = __shfl_up(incl, d);
+        if (lane >= d) incl += o;
+    }
+    if (lane == 63) wave_sum[wave] = incl;
+    __syncthreads();
+    int base = incl - tot;
+    for (int w = 0; w < wave; ++w) base += wave_sum[w];
+    if (e_own < num_experts) {
+        expert_offsets[e_own] = base;
+        for (int w = 0; w < kDispatchWaves; ++w) {
+            const int c = cnt[w * num_experts + e_own];
+            cnt[w * num_experts + e_own] = base;
+            base += c;
         }
-        expert_offsets[num_experts] = run;
+        if (e_own == num_experts - 1) expert_offsets[num_experts] = base;
     }
     __syncthreads();
     // stable placement: 64 routes per step in route order; lanes with equal experts
@@ -164,13 +211,12 @@ __global__ __launch_bounds__(256) void moe_gather_q8_1_kernel(const uint8_t *__r
 // Decode batches (at most kMoeDecodeRoutes routes): quantize, top-k, dispatch and
 // gather in one launch.  Workgroup r owns route r = t * top_k + k: it issues the
 // loads of token t's fp32 row first, then recomputes the top-k of every token
-// (top_k_token over logits staged in LDS: the same bits as moe_top_k_kernel) and
+// (top_k_token, a wave per token: the same bits as moe_top_k_kernel) and
 // the stable position of each route
 //   pos(r) = #{r' : e(r') < e(r)} + #{r' < r : e(r') = e(r)}
 // (moe_dispatch_kernel's order), and quantizes the row into Q8_1 row pos(r) of xp
 // with the quantizer's group arithmetic (quantize_group8: the bytes of
 // launch_quantize_q8_1 + moe_gather_q8_1).  Workgroup 0 also writes the tables.
-constexpr int kDecodeLogitsLds = 4096;  // logits staged in LDS up to this many
 constexpr int kDecodeRowRegs = 4;       // float4 per thread loaded up front (1024 threads' worth per step)
 
 __device__ __forceinline__ void quantize_store_q8_1(float4 v, int i0, uint8_t *__restrict__ xp, int R, int pos) {
@@ -189,7 +235,6 @@ __global__ __launch_bounds__(256) void moe_route_decode_kernel(
     __shared__ int s_ids[kMoeDecodeRoutes];
     __shared__ float s_w[kMoeDecodeRoutes];
     __shared__ int s_pos[kMoeDecodeRoutes];
-    __shared__ float s_logits[kDecodeLogitsLds];
     const int R = num_tokens * top_k;
     const int r_own = blockIdx.x;
     const bool lead = blockIdx.x == 0;
@@ -202,15 +247,10 @@ __global__ __launch_bounds__(256) void moe_route_decode_kernel(
         const int i0 = (threadIdx.x + i * 256) * 4;
         xv[i] = i0 < hidden ? *reinterpret_cast<const float4 *>(row + i0) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    // 2) top-k of every token
-    const int n_logits = num_tokens * num_experts;
-    const bool staged = n_logits <= kDecodeLogitsLds;
-    if (staged)
-        for (int i = threadIdx.x; i < n_logits; i += blockDim.x) s_logits[i] = logits[i];
-    __syncthreads();
-    const float *lg = staged ? s_logits : logits;
-    for (int t = threadIdx.x; t < num_tokens; t += blockDim.x)
-        top_k_token(lg + (size_t)t * num_experts, num_experts, top_k, s_w + t * top_k, s_ids + t * top_k);
+    // 2) top-k of every token, one wave per token
+    for (int t = threadIdx.x >> 6; t < num_tokens; t += blockDim.x >> 6)
+        top_k_token(logits + (size_t)t * num_experts, num_experts, top_k, s_w + t * top_k, s_ids + t * top_k,
+                    threadIdx.x & 63);
     __syncthreads();
     // 3) stable positions (ids clamped to a valid expert, as in moe_dispatch_kernel)
     for (int r = threadIdx.x; r < R; r += blockDim.x) {
@@ -274,8 +314,8 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float *__restric
 
 hipError_t launch_moe_top_k(const float *logits, float *weights, int *ids, int num_tokens, int num_experts,
                             int top_k, hipStream_t stream) {
-    hipLaunchKernelGGL(moe_top_k_kernel, dim3((num_tokens + 63) / 64), dim3(64), 0, stream, logits, weights, ids,
-                       num_tokens, num_experts, top_k);
+    hipLaunchKernelGGL(moe_top_k_kernel, dim3((num_tokens + kTopKWaves - 1) / kTopKWaves), dim3(64 * kTopKWaves), 0,
+                       stream, logits, weights, ids, num_tokens, num_experts, top_k);
     return hipGetLastError();
 }
 

@@ -135,6 +135,7 @@ MOE_DECODE_CASES = [  # T, H, I, E, top_k
     (2, 512, 5120, 4, 2),      # down projection K = 5120: two K slices
     (1, 9216, 256, 4, 2),      # gate|up K = 9216: three K slices
     (3, 16384, 128, 3, 1),     # gate|up K = 16384: four K slices
+    (16, 128, 128, 32, 25),    # 400 routes: routing in four launches, then the routed GEMVs
 ]
 
 
@@ -168,6 +169,37 @@ def test_moe_top_k_ties_take_smaller_id(dev):
     ids = torch.empty(12, dtype=torch.int32, device=dev)
     capi.moe_top_k(to_dev(lg, dev), w, ids, 4, 8, 3)
     assert host(ids).reshape(4, 3).tolist() == [[0, 1, 2], [2, 5, 0], [0, 1, 2], [7, 0, 1]]
+
+
+@pytest.mark.parametrize("E,top_k", [(8, 3), (64, 8), (256, 8), (1024, 32), (70, 5)])
+def test_moe_top_k_special_values(E, top_k, dev):
+    """The wave-per-token selection reproduces the reference's sequential scan on the
+    rows that tell them apart: NaN at expert 0 (kept every round) and elsewhere
+    (never chosen), all -inf (expert 0 re-selected), a single finite logit, +-0 ties,
+    and ties spread over the whole row (smaller id first)."""
+    import torch
+    note(f"moe_top_k special E={E} k={top_k}")
+    rng = np.random.default_rng(E + top_k)
+    rows = [rng.standard_normal(E).astype(np.float32) for _ in range(8)]
+    rows[0][0] = np.nan
+    rows[1][[1, E // 2, E - 1]] = np.nan
+    rows[2][:] = -np.inf
+    rows[3][:] = -np.inf
+    rows[3][E - 1] = 0.5
+    rows[4][:] = 0.0
+    rows[4][1::2] = -0.0
+    rows[5][:] = np.float32(1.25)
+    rows[6][rng.permutation(E)[: min(E, 3 * top_k)]] = np.float32(9.0)  # many equal maxima
+    rows[7][0] = -np.inf
+    lg = np.stack(rows).astype(np.float32)
+    T = lg.shape[0]
+    w = torch.empty(T * top_k, dtype=torch.float32, device=dev)
+    ids = torch.empty(T * top_k, dtype=torch.int32, device=dev)
+    capi.moe_top_k(to_dev(lg, dev), w, ids, T, E, top_k)
+    with np.errstate(invalid="ignore"):  # NaN rows give NaN weights on both sides
+        ref_ids, ref_w = oracle_np.moe_top_k(lg, top_k)
+    assert np.array_equal(host(ids).reshape(T, top_k), ref_ids)
+    np.testing.assert_allclose(host(w).reshape(T, top_k), ref_w, rtol=2e-6, atol=1e-7, equal_nan=True)
 
 
 @pytest.mark.parametrize("T,H,I,E,top_k", MOE_CASES)
