@@ -101,7 +101,7 @@ __device__ __forceinline__ float dpp(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
 }
 
-// NV independent 64-lane sums at once (NV a power of two, <= 16).  Transposed
+// NV independent 64-lane sums at once (NV a power of two, <= 32).  Transposed
 // butterfly: in round r (distance 32 >> r) each lane keeps one of every pair of its
 // values, adds its partner's copy of it and sends the other, so the values per lane
 // halve while the lanes per partial double.  After log2(NV) rounds every lane holds
@@ -109,8 +109,8 @@ __device__ __forceinline__ float dpp(float v) {
 // remaining 64 / NV lanes that share it finishes the sum.  Returns the lane's sum.
 template <int NV>
 __device__ __forceinline__ float multi_sum(float (&v)[NV], int lane) {
-    static_assert(NV == 1 || NV == 2 || NV == 4 || NV == 8 || NV == 16, "NV");
-    constexpr int R = NV == 1 ? 0 : NV == 2 ? 1 : NV == 4 ? 2 : NV == 8 ? 3 : 4;
+    static_assert(NV == 1 || NV == 2 || NV == 4 || NV == 8 || NV == 16 || NV == 32, "NV");
+    constexpr int R = NV == 1 ? 0 : NV == 2 ? 1 : NV == 4 ? 2 : NV == 8 ? 3 : NV == 16 ? 4 : 5;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const int dist = 32 >> r;
@@ -139,7 +139,7 @@ __device__ __forceinline__ float multi_sum(float (&v)[NV], int lane) {
 // Value index whose sum multi_sum<NV> leaves in `lane`.
 template <int NV>
 __device__ __forceinline__ int multi_sum_index(int lane) {
-    constexpr int R = NV == 1 ? 0 : NV == 2 ? 1 : NV == 4 ? 2 : NV == 8 ? 3 : 4;
+    constexpr int R = NV == 1 ? 0 : NV == 2 ? 1 : NV == 4 ? 2 : NV == 8 ? 3 : NV == 16 ? 4 : 5;
     int idx = 0;
 #pragma unroll
     for (int r = 0; r < R; ++r) idx |= ((lane >> (5 - r)) & 1) << r;
@@ -713,13 +713,17 @@ __device__ __forceinline__ void finish_f32_s(uint8_t *xs, uint8_t *__restrict__ 
 // of gemv_q4_0_q8_1_kernel.
 // ROUTED: a routed launch (RouteArgs) over E stacked split-layout experts (one
 // nibble plane over all E * N rows, then one scale plane), Q8_1 input.
-template <int M, int U, int JS, int RG, bool FUSED, int EARLY, bool ROUTED = false>
+// R2 (K <= 2048, one K slice): a lane's second block slot, otherwise past the row
+// end, takes the same block of the row U further on: a wave covers 2U rows.
+template <int M, int U, int JS, int RG, bool FUSED, int EARLY, bool ROUTED = false, bool R2 = false>
 __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *__restrict__ w,
                                                                 const void *__restrict__ xin,
                                                                 uint8_t *__restrict__ xq_out,
                                                                 float *__restrict__ y, int K, int N,
                                                                 RouteArgs ra) {
     static_assert(!(ROUTED && FUSED), "routed launches take Q8_1 route rows");
+    static_assert(!R2 || JS == 1, "paired rows: one K slice");
+    constexpr int kRowsW = R2 ? 2 * U : U;  // rows per wave
     extern __shared__ __align__(16) uint8_t xs[];  // M * K/32 records of kRecS bytes + 1 spare
     __shared__ float part[JS > 1 ? RG * JS * U * M : 1];
 
@@ -732,7 +736,7 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
     const int bk0 = 128 * js + lane;       // this lane's two blocks
     const int bk1 = bk0 + 64;
     const int c0 = min(bk0, nb - 1), c1 = min(bk1, nb - 1);
-    const int r0 = (blockIdx.x * RG + rg) * U;
+    const int r0 = (blockIdx.x * RG + rg) * kRowsW;
     const int n_items = FUSED ? 2 * nb : M * nb;
     const int rounds = (n_items + kThreadsWG - 1) / kThreadsWG;
     RouteTile rt{0, 0, 0, M, M};
@@ -771,10 +775,12 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const size_t base = (row0 + (size_t)min(r0 + u, N - 1)) * nb;
+        const size_t base1 = R2 ? (row0 + (size_t)min(r0 + U + u, N - 1)) * nb : base;  // slot 1's row
+        const int cs1 = R2 ? c0 : c1;                                                       // slot 1's block
         wq[u][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4a16 *>(w + (base + c0) * 16));
-        wq[u][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4a16 *>(w + (base + c1) * 16));
+        wq[u][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4a16 *>(w + (base1 + cs1) * 16));
         wd[u][0] = dpl[base + c0];
-        wd[u][1] = dpl[base + c1];
+        wd[u][1] = dpl[base1 + cs1];
     }
     __builtin_amdgcn_sched_barrier(0);
     // 3) the early items (routed launches: before the chunk loop, so that they are not
@@ -799,7 +805,7 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
         const int bk0 = ROUTED ? 128 * js + lane : bk0_o;
         const int bk1 = bk0 + 64;
         const int c0 = min(bk0, nb - 1), c1 = min(bk1, nb - 1);
-        const int r0 = ROUTED ? (int)(blockIdx.x * RG + rg) * U : r0_o;
+        const int r0 = ROUTED ? (int)(blockIdx.x * RG + rg) * kRowsW : r0_o;
         // 3) activation records of the whole K range in LDS, once per workgroup (routed:
         //    per chunk of routes)
         for (int r = (ROUTED && again) ? 0 : EARLY; r < rounds; ++r) {  // the rest, load-then-use
@@ -819,9 +825,9 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
         __syncthreads();
 
         // 4) rows in load order
-        float acc[U][M];
+        float acc[kRowsW][M];
 #pragma unroll
-        for (int u = 0; u < U; ++u)
+        for (int u = 0; u < kRowsW; ++u)
 #pragma unroll
             for (int m = 0; m < M; ++m) acc[u][m] = 0.0f;
 
@@ -846,8 +852,8 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
                 if (m < mcc) {
 #pragma unroll
                     for (int k = 0; k < 2; ++k) {
-                        const bool live = (k ? bk1 : bk0) < nb;
-                        const uint8_t *rec = xs + ((size_t)m * nb + (k ? c1 : c0)) * kRecS;
+                        const bool live = ((k && !R2) ? bk1 : bk0) < nb;
+                        const uint8_t *rec = xs + ((size_t)m * nb + ((k && !R2) ? c1 : c0)) * kRecS;
                         const u32x4a16 h4 = *reinterpret_cast<const u32x4a16 *>(rec);
                         const u32x4a16 l4 = *reinterpret_cast<const u32x4a16 *>(rec + 16);
                         const u32x2a8 c2 = *reinterpret_cast<const u32x2a8 *>(rec + 32);
@@ -857,7 +863,7 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
                             const uint32_t q[4] = {wq[u][k].x, wq[u][k].y, wq[u][k].z, wq[u][k].w};
                             const int32_t sv = block_sumi(q, hi, lo, ns[u][k]);
                             const float v = dw[u][k] * fmaf((float)sv, __uint_as_float(c2.x), __uint_as_float(c2.y));
-                            acc[u][m] += live ? v : 0.0f;
+                            acc[u + (R2 ? k * U : 0)][m] += live ? v : 0.0f;
                         }
                     }
                 }
@@ -867,8 +873,8 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
         for (int u = 0; u < U; ++u) {
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
-                const bool live = (k ? bk1 : bk0) < nb;
-                const int cb = k ? c1 : c0;
+                const bool live = ((k && !R2) ? bk1 : bk0) < nb;
+                const int cb = (k && !R2) ? c1 : c0;
                 const uint32_t q[4] = {wq[u][k].x, wq[u][k].y, wq[u][k].z, wq[u][k].w};
                 const int32_t ns = nib_sum128(q);
                 const float dw = __half2float(__ushort_as_half((unsigned short)wd[u][k]));
@@ -881,20 +887,20 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
                     const uint32_t hi[4] = {h4.x, h4.y, h4.z, h4.w}, lo[4] = {l4.x, l4.y, l4.z, l4.w};
                     const int32_t sv = block_sumi(q, hi, lo, ns);
                     const float v = dw * fmaf((float)sv, __uint_as_float(c2.x), __uint_as_float(c2.y));
-                    acc[u][m] += live ? v : 0.0f;
+                    acc[u + (R2 ? k * U : 0)][m] += live ? v : 0.0f;
                 }
             }
         }
         }
 
-        constexpr int NV = pow2_at_least(U * M);
+        constexpr int NV = pow2_at_least(kRowsW * M);
         float v[NV];
 #pragma unroll
-        for (int i = 0; i < NV; ++i) v[i] = i < U * M ? acc[i / M][i % M] : 0.0f;
+        for (int i = 0; i < NV; ++i) v[i] = i < kRowsW * M ? acc[i / M][i % M] : 0.0f;
         const float s = multi_sum<NV>(v, lane);
         const int idx = multi_sum_index<NV>(lane);
         const int u = idx / M, m = idx % M;
-        const bool owner = (lane & (64 / NV - 1)) == 0 && idx < U * M;
+        const bool owner = (lane & (64 / NV - 1)) == 0 && idx < kRowsW * M;
         if constexpr (JS == 1) {
             if (owner && r0 + u < N && m < mcc) y[(ROUTED ? routed_row(ra, m0c + m) : (size_t)m) * ldy + r0 + u] = s;
         } else {
@@ -927,10 +933,12 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4s_kernel(const uint8_t *_
             if constexpr (M <= 2) {  // (as in gemv_q4_0_q8_1_kernel)
                 for (int u = 0; u < U; ++u) {
                     const size_t base = (row0 + (size_t)min(r0 + u, N - 1)) * nb;
+                    const size_t base1 = R2 ? (row0 + (size_t)min(r0 + U + u, N - 1)) * nb : base;
+                    const int cs1 = R2 ? c0 : c1;
                     wq[u][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4a16 *>(w + (base + c0) * 16));
-                    wq[u][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4a16 *>(w + (base + c1) * 16));
+                    wq[u][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4a16 *>(w + (base1 + cs1) * 16));
                     wd[u][0] = dpl[base + c0];
-                    wd[u][1] = dpl[base + c1];
+                    wd[u][1] = dpl[base1 + cs1];
                 }
             }
         }
@@ -1000,14 +1008,15 @@ constexpr int rg_pick() {
 }
 
 // Routed launches (ROUTED) run over the gy expert slots of `ra`.
-template <bool SPLIT, int M, int U, int JS, bool FUSED, int EARLY, bool ROUTED = false>
+template <bool SPLIT, int M, int U, int JS, bool FUSED, int EARLY, bool ROUTED = false, bool R2 = false>
 hipError_t launch_cfg(const void *w, const void *xin, uint8_t *xq_out, float *y, int K, int N, hipStream_t stream,
                       const RouteArgs &ra = RouteArgs{}, int gy = 1) {
     constexpr int RG = rg_pick<SPLIT, M, JS, FUSED, ROUTED>();
-    const int groups = (N + U - 1) / U;
+    constexpr int kRowsW = R2 ? 2 * U : U;
+    const int groups = (N + kRowsW - 1) / kRowsW;
     const int blocks = (groups + RG - 1) / RG;
     const size_t smem = SPLIT ? ((size_t)M * (K / 32) + 1) * kRecS : ((size_t)M * (K / 64) + 1) * kRec;
-    const void *kern = SPLIT ? (const void *)gemv_q4s_kernel<M, U, JS, RG, FUSED, EARLY, ROUTED>
+    const void *kern = SPLIT ? (const void *)gemv_q4s_kernel<M, U, JS, RG, FUSED, EARLY, ROUTED, R2>
                              : (const void *)gemv_q4_0_q8_1_kernel<M, U, JS, RG, FUSED, EARLY, ROUTED>;
     if (smem > 64 * 1024) {
         // Raise this instantiation's dynamic-LDS limit to what the call needs.
@@ -1015,7 +1024,7 @@ hipError_t launch_cfg(const void *w, const void *xin, uint8_t *xq_out, float *y,
         if (e != hipSuccess) return e;
     }
     if constexpr (SPLIT) {
-        hipLaunchKernelGGL((gemv_q4s_kernel<M, U, JS, RG, FUSED, EARLY, ROUTED>), dim3(blocks, gy),
+        hipLaunchKernelGGL((gemv_q4s_kernel<M, U, JS, RG, FUSED, EARLY, ROUTED, R2>), dim3(blocks, gy),
                            dim3(64 * JS * RG), smem, stream, (const uint8_t *)w, xin, xq_out, y, K, N, ra);
     } else {
         hipLaunchKernelGGL((gemv_q4_0_q8_1_kernel<M, U, JS, RG, FUSED, EARLY, ROUTED>), dim3(blocks, gy),
@@ -1024,7 +1033,7 @@ hipError_t launch_cfg(const void *w, const void *xin, uint8_t *xq_out, float *y,
     return hipGetLastError();
 }
 
-template <bool SPLIT, int M, int U, int JS, bool FUSED, bool ROUTED = false>
+template <bool SPLIT, int M, int U, int JS, bool FUSED, bool ROUTED = false, bool R2 = false>
 hipError_t launch_js(const void *w, const void *xin, uint8_t *xq_out, float *y, int K, int N, hipStream_t stream,
                      const RouteArgs &ra = RouteArgs{}, int gy = 1) {
     constexpr int RG = rg_pick<SPLIT, M, JS, FUSED, ROUTED>();
@@ -1034,18 +1043,25 @@ hipError_t launch_js(const void *w, const void *xin, uint8_t *xq_out, float *y, 
     // the weights (its chunk loop keeps the 36 raw weight dwords of four rows live;
     // two early rounds spill at 1024 threads' 128 registers).
     if constexpr (ROUTED && !SPLIT && M == 4 && JS == 4 && RG == 4)
-        return launch_cfg<SPLIT, M, U, JS, FUSED, 1, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy);
-    if (rounds <= 1) return launch_cfg<SPLIT, M, U, JS, FUSED, 1, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy);
-    if (rounds <= 2) return launch_cfg<SPLIT, M, U, JS, FUSED, 2, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy);
-    return launch_cfg<SPLIT, M, U, JS, FUSED, 4, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy);
+        return launch_cfg<SPLIT, M, U, JS, FUSED, 1, ROUTED, R2>(w, xin, xq_out, y, K, N, stream, ra, gy);
+    if (rounds <= 1) return launch_cfg<SPLIT, M, U, JS, FUSED, 1, ROUTED, R2>(w, xin, xq_out, y, K, N, stream, ra, gy);
+    if (rounds <= 2) return launch_cfg<SPLIT, M, U, JS, FUSED, 2, ROUTED, R2>(w, xin, xq_out, y, K, N, stream, ra, gy);
+    return launch_cfg<SPLIT, M, U, JS, FUSED, 4, ROUTED, R2>(w, xin, xq_out, y, K, N, stream, ra, gy);
 }
 
+#ifndef JJO_Q4S_R2
+#define JJO_Q4S_R2 1
+#endif
 template <bool SPLIT, int M, int U, bool FUSED, bool ROUTED = false>
 hipError_t launch_m(const void *w, const void *xin, uint8_t *xq_out, float *y, int K, int N, hipStream_t stream,
                     const RouteArgs &ra = RouteArgs{}, int gy = 1) {
     const int js = (K / 64 + 63) / 64;
     switch (js) {
-        case 1: return launch_js<SPLIT, M, U, 1, FUSED, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy);
+        case 1:
+            // split rows of at most 64 blocks: two rows per wave instruction (R2)
+            if (SPLIT && K <= 2048 && JJO_Q4S_R2)
+                return launch_js<SPLIT, M, U, 1, FUSED, ROUTED, SPLIT>(w, xin, xq_out, y, K, N, stream, ra, gy);
+            return launch_js<SPLIT, M, U, 1, FUSED, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy);
         case 2: return launch_js<SPLIT, M, U, 2, FUSED, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy);
         case 3:
             return launch_js<SPLIT, M, (SPLIT && M == 1 && !FUSED) ? 2 : U, 3, FUSED, ROUTED>(w, xin, xq_out, y, K, N,
