@@ -375,13 +375,18 @@ __device__ __forceinline__ int opaque_int(int v) {
 // FUSED: `xin` is the fp32 activation [K] (M = 1) instead of Q8_1 blocks and
 // `xq_out` (optional) receives its Q8_1 bytes (written by workgroup 0).
 // ROUTED: a routed launch (RouteArgs), M routes per workgroup, Q8_1 input.
-template <int M, int U, int JS, int RG, bool FUSED, int EARLY, bool ROUTED = false>
+// R2 (K <= 2048, one K slice): rows hold at most 32 block pairs, so lanes 32..63 take
+// the rows U further on: a wave covers 2U rows (each lane's sums for the other half's
+// rows are zero in the wave reduction).
+template <int M, int U, int JS, int RG, bool FUSED, int EARLY, bool ROUTED = false, bool R2 = false>
 __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint8_t *__restrict__ w,
                                                                       const void *__restrict__ xin,
                                                                       uint8_t *__restrict__ xq_out,
                                                                       float *__restrict__ y, int K, int N,
                                                                       RouteArgs ra) {
     static_assert(!(ROUTED && FUSED), "routed launches take Q8_1 route rows");
+    static_assert(!R2 || JS == 1, "paired rows: one K slice");
+    constexpr int kRowsW = R2 ? 2 * U : U;  // rows per wave
     extern __shared__ __align__(16) uint8_t xs[];  // M * K/64 records of kRec bytes + 1 spare
     __shared__ float part[JS > 1 ? RG * JS * U * M : 1];
 
@@ -392,10 +397,11 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
     const int rg = wave / JS;              // row group inside the workgroup
     const int nb = K / kQK;
     const int P = nb >> 1;                 // block pairs per row
-    const int p = lane + 64 * js;          // this lane's pair
+    const int p = R2 ? (lane & 31) : lane + 64 * js;  // this lane's pair
+    const int hrow = R2 ? (lane >> 5) * U : 0;         // R2: lanes 32..63 on rows U further
     const bool live = p < P;
     const size_t row_bytes = (size_t)nb * kQ4BlockBytes;
-    const int r0 = (blockIdx.x * RG + rg) * U;
+    const int r0 = (blockIdx.x * RG + rg) * kRowsW;
     const int n_items = FUSED ? 2 * nb : M * nb;
     const int rounds = (n_items + kThreadsWG - 1) / kThreadsWG;
     RouteTile rt{0, 0, 0, M, M};
@@ -433,7 +439,7 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
         const int pl = min(p, P - 1);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int rr = min(r0 + u, N - 1);
+            const int rr = min(r0 + hrow + u, N - 1);
             load_pair(wb[u], w + (size_t)rr * row_bytes + (size_t)pl * 36);
         }
     }
@@ -459,9 +465,9 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
         const int lane = ROUTED ? (tid & 63) : lane_o;
         const int js = ROUTED ? (tid >> 6) % JS : js_o;
         const int rg = ROUTED ? (tid >> 6) / JS : rg_o;
-        const int p = ROUTED ? lane + 64 * js : p_o;
+        const int p = ROUTED ? (R2 ? (lane & 31) : lane + 64 * js) : p_o;
         const bool live = p < P;
-        const int r0 = ROUTED ? (int)(blockIdx.x * RG + rg) * U : r0_o;
+        const int r0 = ROUTED ? (int)(blockIdx.x * RG + rg) * kRowsW : r0_o;
         // 3) activation planes of the whole K range in LDS, once per workgroup (routed:
         //    per chunk of routes)
         for (int r = (ROUTED && again) ? 0 : EARLY; r < rounds; ++r) {  // the rest, load-then-use
@@ -574,14 +580,19 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
 
         // All U * M sums of the wave in one transposed reduction; lane `owner` of each
         // group that shares a value holds its sum.
-        constexpr int NV = pow2_at_least(U * M);
+        constexpr int NV = pow2_at_least(kRowsW * M);
         float v[NV];
 #pragma unroll
-        for (int i = 0; i < NV; ++i) v[i] = i < U * M ? acc[i / M][i % M] : 0.0f;
+        for (int i = 0; i < NV; ++i) {
+            // (R2: values U*M.. are the rows U further on, held by lanes 32..63)
+            const int ii = i % (U * M);
+            const bool mine = !R2 || ((i >= U * M) == (lane >= 32));
+            v[i] = i < kRowsW * M && mine ? acc[ii / M][ii % M] : 0.0f;
+        }
         const float s = multi_sum<NV>(v, lane);
         const int idx = multi_sum_index<NV>(lane);
         const int u = idx / M, m = idx % M;
-        const bool owner = (lane & (64 / NV - 1)) == 0 && idx < U * M;
+        const bool owner = (lane & (64 / NV - 1)) == 0 && idx < kRowsW * M;
         if constexpr (JS == 1) {
             if (owner && r0 + u < N && m < mcc) y[(ROUTED ? routed_row(ra, m0c + m) : (size_t)m) * ldy + r0 + u] = s;
         } else {
@@ -617,7 +628,8 @@ __global__ __launch_bounds__(64 * JS * RG) void gemv_q4_0_q8_1_kernel(const uint
                 // occupancy, for a loop that only a tie-broken top-k repeat reaches.
                 const int pl = min(p, P - 1);
                 for (int u = 0; u < U; ++u)
-                    load_pair(wb[u], w + (size_t)min(r0 + u, N - 1) * row_bytes + (size_t)pl * 36);
+                    load_pair(wb[u], w + (size_t)min(r0 + (R2 ? (lane >> 5) * U : 0) + u, N - 1) * row_bytes +
+                                         (size_t)pl * 36);
             }
         }
     }
@@ -1017,7 +1029,7 @@ hipError_t launch_cfg(const void *w, const void *xin, uint8_t *xq_out, float *y,
     const int blocks = (groups + RG - 1) / RG;
     const size_t smem = SPLIT ? ((size_t)M * (K / 32) + 1) * kRecS : ((size_t)M * (K / 64) + 1) * kRec;
     const void *kern = SPLIT ? (const void *)gemv_q4s_kernel<M, U, JS, RG, FUSED, EARLY, ROUTED, R2>
-                             : (const void *)gemv_q4_0_q8_1_kernel<M, U, JS, RG, FUSED, EARLY, ROUTED>;
+                             : (const void *)gemv_q4_0_q8_1_kernel<M, U, JS, RG, FUSED, EARLY, ROUTED, R2>;
     if (smem > 64 * 1024) {
         // Raise this instantiation's dynamic-LDS limit to what the call needs.
         hipError_t e = ensure_dynamic_lds(kern, smem);
@@ -1027,7 +1039,7 @@ hipError_t launch_cfg(const void *w, const void *xin, uint8_t *xq_out, float *y,
         hipLaunchKernelGGL((gemv_q4s_kernel<M, U, JS, RG, FUSED, EARLY, ROUTED, R2>), dim3(blocks, gy),
                            dim3(64 * JS * RG), smem, stream, (const uint8_t *)w, xin, xq_out, y, K, N, ra);
     } else {
-        hipLaunchKernelGGL((gemv_q4_0_q8_1_kernel<M, U, JS, RG, FUSED, EARLY, ROUTED>), dim3(blocks, gy),
+        hipLaunchKernelGGL((gemv_q4_0_q8_1_kernel<M, U, JS, RG, FUSED, EARLY, ROUTED, R2>), dim3(blocks, gy),
                            dim3(64 * JS * RG), smem, stream, (const uint8_t *)w, xin, xq_out, y, K, N, ra);
     }
     return hipGetLastError();
@@ -1049,8 +1061,8 @@ hipError_t launch_js(const void *w, const void *xin, uint8_t *xq_out, float *y, 
     return launch_cfg<SPLIT, M, U, JS, FUSED, 4, ROUTED, R2>(w, xin, xq_out, y, K, N, stream, ra, gy);
 }
 
-#ifndef JJO_Q4S_R2
-#define JJO_Q4S_R2 1
+#ifndef JJO_GEMV_R2
+#define JJO_GEMV_R2 1
 #endif
 template <bool SPLIT, int M, int U, bool FUSED, bool ROUTED = false>
 hipError_t launch_m(const void *w, const void *xin, uint8_t *xq_out, float *y, int K, int N, hipStream_t stream,
@@ -1058,9 +1070,13 @@ hipError_t launch_m(const void *w, const void *xin, uint8_t *xq_out, float *y, i
     const int js = (K / 64 + 63) / 64;
     switch (js) {
         case 1:
-            // split rows of at most 64 blocks: two rows per wave instruction (R2)
-            if (SPLIT && K <= 2048 && JJO_Q4S_R2)
-                return launch_js<SPLIT, M, U, 1, FUSED, ROUTED, SPLIT>(w, xin, xq_out, y, K, N, stream, ra, gy);
+            // Rows of at most 64 blocks: two rows per wave instruction (R2), unless that
+            // leaves fewer workgroups than CUs (N=2048 at batch 4: 6.12 against 5.76 us).
+            if (K <= 2048 && JJO_GEMV_R2) {
+                constexpr int kRowsWG = 2 * U * rg_pick<SPLIT, M, 1, FUSED, ROUTED>();
+                if ((int64_t)((N + kRowsWG - 1) / kRowsWG) * gy >= device_cu_count())
+                    return launch_js<SPLIT, M, U, 1, FUSED, ROUTED, true>(w, xin, xq_out, y, K, N, stream, ra, gy);
+            }
             return launch_js<SPLIT, M, U, 1, FUSED, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy);
         case 2: return launch_js<SPLIT, M, U, 2, FUSED, ROUTED>(w, xin, xq_out, y, K, N, stream, ra, gy);
         case 3:
