@@ -364,7 +364,8 @@ int moe_combine_device(void *stream, const float *expert_out, const int32_t *dst
  * y fp32 [T][H].  `workspace` (256-byte aligned) holds every intermediate; its
  * size is moe_q4_0_ffn_workspace_bytes(...).  Seven launches (quantize x, top-k,
  * dispatch, gather, gate|up with SwiGLU and Q8_1, down, combine); at 16 tokens or
- * fewer (H, I <= 16384) five (routing in one launch, gate|up over the active experts
+ * fewer, or at most two routes per active expert on average (H, I <= 16384), five
+ * (routing in one launch -- four above 384 routes --, gate|up over the active experts
  * into an fp32 [R][2I] part of the workspace, SwiGLU + Q8_1, down, combine).  No
  * allocation, asynchronous on `stream`.  H % 128 == 0, I % 128 == 0.
  */
@@ -376,8 +377,9 @@ int moe_q4_0_ffn_forward_device(void *stream, const float *x, const float *logit
                                 int64_t workspace_bytes);
 /* The same FFN on expert weights repacked into the split layout (each of gate, up
  * and down as one [E * rows] matrix, 16-byte aligned); y equals the block_q4_0
- * entry's bit for bit above 16 tokens (below, both are within fp32 rounding of the
- * oracle: the two layouts' GEMVs sum a row in different orders). */
+ * entry's bit for bit where both run the MFMA tiles (on the routed-GEMV path, both are
+ * within fp32 rounding of the oracle: the two layouts' GEMVs sum a row in different
+ * orders). */
 int moe_q4_0s_ffn_forward_device(void *stream, const float *x, const float *logits, const void *w_gate_split,
                                  const void *w_up_split, const void *w_down_split, float *y, int num_tokens,
                                  int hidden_size, int intermediate_size, int num_experts, int top_k, void *workspace,

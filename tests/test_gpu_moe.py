@@ -124,7 +124,15 @@ MOE_CASES = [  # T, H, I, E, top_k
 ]
 # Decode-sized batches: the FFN runs its expert matrices as routed GEMVs (a
 # token's experts are distinct, so no expert holds more than T routes).
-MOE_DECODE_T = 16  # at least the FFN's routed-GEMV token limit
+MOE_DECODE_T = 16  # the FFN's routed-GEMV token limit
+
+
+def _ffn_routed(T, E, top_k):
+    """Whether the FFN runs routed GEMVs: up to MOE_DECODE_T tokens, or at most two
+    routes per active expert on average (many experts)."""
+    R = T * top_k
+    active = min(E, R)
+    return T <= MOE_DECODE_T or -(-R // active) <= 2
 MOE_DECODE_CASES = [  # T, H, I, E, top_k
     (1, 256, 384, 8, 2),       # one route per active expert
     (2, 512, 256, 16, 4),
@@ -420,7 +428,7 @@ def test_moe_ffn_end_to_end(T, H, I, E, top_k, dev):
     y2 = torch.empty(T * H, dtype=torch.float32, device=dev)
     capi.moe_combine(eo, dst, rw, y2, T, H, top_k)
     ref = _oracle_ffn(x, lg, wg, wu, wd, top_k)
-    if T > MOE_DECODE_T:  # the same kernels as the stage entries: the same bits
+    if not _ffn_routed(T, E, top_k):  # the same kernels as the stage entries: the same bits
         assert np.array_equal(y_ffn, host(y2).reshape(T, H))
     else:  # routed GEMVs sum each row in another order than the MFMA tiles
         np.testing.assert_allclose(host(y2).reshape(T, H), ref, rtol=2e-3, atol=2e-3)
@@ -562,7 +570,7 @@ def test_moe_ffn_split_layout(T, H, I, E, top_k, dev):
     capi.moe_ffn(d["x"], d["lg"], sg, su, sd, y2, T, H, I, E, top_k, ws, split=True)
     a, b = host(y1), host(y2)
     assert np.isfinite(a).all()
-    if T > MOE_DECODE_T:
+    if not _ffn_routed(T, E, top_k):
         assert np.array_equal(a, b)
     else:
         ref = _oracle_ffn(x, lg, wg, wu, wd, top_k)
