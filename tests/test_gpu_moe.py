@@ -395,6 +395,27 @@ def _oracle_ffn(x, lg, wg, wu, wd, top_k):
     return oracle_np.moe_combine(eo, dst, w.reshape(-1), top_k)
 
 
+def _ffn_ws_combine(ws, T, H, I, E, top_k, dev):
+    """moe_combine over the FFN workspace's own route weights, sorted-route indices and
+    expert outputs (the workspace carve-up of moe_q4_0_ffn_device: route weights,
+    ids, offsets, src, dst, Q8_1 x, permuted Q8_1 x, Q8_1 mid, expert outputs, each
+    256-byte aligned)."""
+    import torch
+    R = T * top_k
+    sizes = [R * 4, R * 4, (E + 1) * 4, R * 4, R * 4, T * H // 128 * 144, R * H // 128 * 144, R * I // 128 * 144,
+             R * H * 4]
+    offs, o = [], 0
+    for n in sizes:
+        offs.append(o)
+        o += -(-n // 256) * 256
+    rw = ws[offs[0]:offs[0] + R * 4].view(torch.float32)
+    dst = ws[offs[4]:offs[4] + R * 4].view(torch.int32)
+    eo = ws[offs[8]:offs[8] + R * H * 4].view(torch.float32)
+    y = torch.empty(T * H, dtype=torch.float32, device=dev)
+    capi.moe_combine(eo, dst, rw, y, T, H, top_k)
+    return host(y).reshape(T, H)
+
+
 @pytest.mark.parametrize("T,H,I,E,top_k", MOE_CASES + MOE_DECODE_CASES)
 def test_moe_ffn_end_to_end(T, H, I, E, top_k, dev):
     import torch
@@ -432,6 +453,8 @@ def test_moe_ffn_end_to_end(T, H, I, E, top_k, dev):
         assert np.array_equal(y_ffn, host(y2).reshape(T, H))
     else:  # routed GEMVs sum each row in another order than the MFMA tiles
         np.testing.assert_allclose(host(y2).reshape(T, H), ref, rtol=2e-3, atol=2e-3)
+        # the FFN's combine: the bits of moe_combine on its own expert outputs
+        assert np.array_equal(y_ffn, _ffn_ws_combine(ws, T, H, I, E, top_k, dev))
     np.testing.assert_allclose(y_ffn, ref, rtol=2e-3, atol=2e-3)
 
 
@@ -457,6 +480,7 @@ def test_moe_ffn_decode_skewed_routing(T, H, I, E, top_k, dev):
         y = torch.full((T * H,), float("nan"), dtype=torch.float32, device=dev)
         capi.moe_ffn(d["x"], d["lg"], *mats, y, T, H, I, E, top_k, ws, split=split)
         np.testing.assert_allclose(host(y).reshape(T, H), ref, rtol=2e-3, atol=2e-3)
+        assert np.array_equal(host(y).reshape(T, H), _ffn_ws_combine(ws, T, H, I, E, top_k, dev))
 
 
 @pytest.mark.parametrize("T", [1, 3])
@@ -486,6 +510,7 @@ def test_moe_ffn_decode_repeated_expert(T, dev):
         y = torch.full((T * H,), float("nan"), dtype=torch.float32, device=dev)
         capi.moe_ffn(d["x"], d["lg"], *mats, y, T, H, I, E, k, ws, split=split)
         np.testing.assert_allclose(host(y).reshape(T, H), ref, rtol=2e-3, atol=2e-3)
+        assert np.array_equal(host(y).reshape(T, H), _ffn_ws_combine(ws, T, H, I, E, k, dev))
 
 
 def test_moe_ffn_rejects_small_workspace(dev):
