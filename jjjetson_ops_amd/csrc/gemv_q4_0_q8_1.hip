@@ -1015,6 +1015,9 @@ constexpr int rg_for_s() {
 // tokens): only the weight stream is left to hide, and twice as many 512-thread
 // workgroups hide it better (E=8, I=14336, T=1..4: 2-6% per FFN step; 2- and
 // 4-route chunks lose 1-15% at 2 row groups).
+#ifndef JJO_RT_RG1_M1
+#define JJO_RT_RG1_M1 0  // one K slice, one route per chunk: 0 = the dense kernel's choice
+#endif
 #ifndef JJO_RT_RG4_M1
 #define JJO_RT_RG4_M1 2
 #endif
@@ -1023,6 +1026,7 @@ constexpr int rg_pick() {
     if (ROUTED && JS == 2) return JJO_RT_RG2;
     if (ROUTED && JS == 3) return JJO_RT_RG3;
     if (ROUTED && JS == 4 && M == 1) return JJO_RT_RG4_M1;
+    if (ROUTED && JS == 1 && M == 1 && JJO_RT_RG1_M1 > 0) return JJO_RT_RG1_M1;
     if (ROUTED && JS == 4) return (!SPLIT && M == 4) ? JJO_RT_RG4_BLK_M4 : JJO_RT_RG4;
     return SPLIT ? rg_for_s<M, JS, FUSED>() : rg_for<M, JS, FUSED>();
 }
