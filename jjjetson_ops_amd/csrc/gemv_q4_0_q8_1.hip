@@ -1011,15 +1011,18 @@ constexpr int rg_for_s() {
 #ifndef JJO_RT_RG4_BLK_M4
 #define JJO_RT_RG4_BLK_M4 4
 #endif
-// One route per chunk (at most one route per active expert, e.g. E=8 top-2 at 1-4
-// tokens): only the weight stream is left to hide, and twice as many 512-thread
-// workgroups hide it better (E=8, I=14336, T=1..4: 2-6% per FFN step; 2- and
-// 4-route chunks lose 1-15% at 2 row groups).
 #ifndef JJO_RT_RG1_M1
 #define JJO_RT_RG1_M1 0  // one K slice, one route per chunk: 0 = the dense kernel's choice
 #endif
 #ifndef JJO_RT_RG1_MX
 #define JJO_RT_RG1_MX 0  // one K slice, 2- and 4-route chunks: 0 = the dense kernel's choice
+#endif
+// One route per chunk (at most one route per active expert, e.g. E=8 top-2 at 1-4
+// tokens) at three or four K slices: only the weight stream is left to hide, and
+// twice as many 2-row-group workgroups hide it better (E=8 down projection, T=1..4:
+// I=14336 2-6%, I=11008 1-3% per FFN step; 2- and 4-route chunks lose 1-15% at 2).
+#ifndef JJO_RT_RG3_M1
+#define JJO_RT_RG3_M1 2
 #endif
 #ifndef JJO_RT_RG4_M1
 #define JJO_RT_RG4_M1 2
@@ -1027,6 +1030,7 @@ constexpr int rg_for_s() {
 template <bool SPLIT, int M, int JS, bool FUSED, bool ROUTED>
 constexpr int rg_pick() {
     if (ROUTED && JS == 2) return JJO_RT_RG2;
+    if (ROUTED && JS == 3 && M == 1 && JJO_RT_RG3_M1 > 0) return JJO_RT_RG3_M1;
     if (ROUTED && JS == 3) return JJO_RT_RG3;
     if (ROUTED && JS == 4 && M == 1) return JJO_RT_RG4_M1;
     if (ROUTED && JS == 1 && M == 1 && JJO_RT_RG1_M1 > 0) return JJO_RT_RG1_M1;

@@ -536,6 +536,7 @@ def _split_stack(w_dev, rows, K, dev):
 @pytest.mark.parametrize("counts,N,K", [([1, 129, 0, 31, 160, 32, 33, 7], 256, 512), ([3, 2, 1, 4], 384, 512),
                                         ([200, 0, 5], 300, 512), ([0, 7, 0, 1], 100, 512), ([32], 256, 512),
                                         ([2, 0, 9, 1], 256, 5120), ([5, 1], 96, 14336),
+                                        ([1, 0, 1, 1], 100, 11008), ([1, 1], 100, 14336), ([2, 0, 1], 64, 11008),
                                         ([0] * 200 + [3] + [0] * 50 + [7, 1] + [0] * 11, 64, 512)])
 def test_grouped_split_layout(counts, N, K, dev):
     """The grouped GEMM on split-layout experts equals the block_q4_0 launch bit for
