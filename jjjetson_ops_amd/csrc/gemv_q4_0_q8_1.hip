@@ -1021,6 +1021,9 @@ constexpr int rg_for_s() {
 // tokens) at three or four K slices: only the weight stream is left to hide, and
 // twice as many 2-row-group workgroups hide it better (E=8 down projection, T=1..4:
 // I=14336 2-6%, I=11008 1-3% per FFN step; 2- and 4-route chunks lose 1-15% at 2).
+#ifndef JJO_RT_RG2_M1
+#define JJO_RT_RG2_M1 0  // two K slices, one route per chunk: 0 = JJO_RT_RG2
+#endif
 #ifndef JJO_RT_RG3_M1
 #define JJO_RT_RG3_M1 2
 #endif
@@ -1029,6 +1032,7 @@ constexpr int rg_for_s() {
 #endif
 template <bool SPLIT, int M, int JS, bool FUSED, bool ROUTED>
 constexpr int rg_pick() {
+    if (ROUTED && JS == 2 && M == 1 && JJO_RT_RG2_M1 > 0) return JJO_RT_RG2_M1;
     if (ROUTED && JS == 2) return JJO_RT_RG2;
     if (ROUTED && JS == 3 && M == 1 && JJO_RT_RG3_M1 > 0) return JJO_RT_RG3_M1;
     if (ROUTED && JS == 3) return JJO_RT_RG3;
