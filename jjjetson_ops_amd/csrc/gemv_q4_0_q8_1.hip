@@ -1163,6 +1163,15 @@ hipError_t launch_gemv_q4s_fused(const void *w, const float *x, void *xq_out, fl
 #ifndef JJO_RT_MT4_MAXK_SPLIT
 #define JJO_RT_MT4_MAXK_SPLIT 16384
 #endif
+// Rows per wave of the one-route routed instances: split as the dense decode
+// kernel; block_q4_0 at 4 instead of 2 (E=8 top-2 FFN T=4: 142.9 -> 138.7 us; split
+// at 2 or 8 and block_q4_0 at 1 were slower).
+#ifndef JJO_RT_U1_SPLIT
+#define JJO_RT_U1_SPLIT JJO_Q4S_U1
+#endif
+#ifndef JJO_RT_U1_BLOCK
+#define JJO_RT_U1_BLOCK 4
+#endif
 int gemv_routed_chunk(int max_routes_per_expert, int K, bool split) {
     const int cap = split && K > JJO_RT_MT4_MAXK_SPLIT ? 2 : 4;
     const int mt = max_routes_per_expert <= 1 ? 1 : max_routes_per_expert <= 2 ? 2 : 4;
@@ -1179,13 +1188,13 @@ hipError_t launch_gemv_routed(const void *w, const void *w2, const void *xq, con
     const int gy = slots * (w2 != nullptr ? 2 : 1);
     if (split) {
         switch (mt) {
-            case 1: return launch_m<true, 1, JJO_Q4S_U1, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
+            case 1: return launch_m<true, 1, JJO_RT_U1_SPLIT, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
             case 2: return launch_m<true, 2, 2, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
             default: return launch_m<true, 4, 4, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
         }
     }
     switch (mt) {
-        case 1: return launch_m<false, 1, kU1, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
+        case 1: return launch_m<false, 1, JJO_RT_U1_BLOCK, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
         case 2: return launch_m<false, 2, 2, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
         default: return launch_m<false, 4, kU4, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
     }
