@@ -1172,6 +1172,21 @@ hipError_t launch_gemv_q4s_fused(const void *w, const float *x, void *xq_out, fl
 #ifndef JJO_RT_U1_BLOCK
 #define JJO_RT_U1_BLOCK 4
 #endif
+// Rows per wave of the 2- and 4-route instances: 2-route chunks at 4 rows (E=8 top-2
+// FFN T=8: 210.9 -> 197.0 us block, 202.0 -> 193.3 split; 1 row 252-254); 4-route
+// chunks at 2 rows were slower (T=16 250.8 -> 294.8).
+#ifndef JJO_RT_U2_SPLIT
+#define JJO_RT_U2_SPLIT 4
+#endif
+#ifndef JJO_RT_U2_BLOCK
+#define JJO_RT_U2_BLOCK 4
+#endif
+#ifndef JJO_RT_U4_SPLIT
+#define JJO_RT_U4_SPLIT 4
+#endif
+#ifndef JJO_RT_U4_BLOCK
+#define JJO_RT_U4_BLOCK kU4
+#endif
 int gemv_routed_chunk(int max_routes_per_expert, int K, bool split) {
     const int cap = split && K > JJO_RT_MT4_MAXK_SPLIT ? 2 : 4;
     const int mt = max_routes_per_expert <= 1 ? 1 : max_routes_per_expert <= 2 ? 2 : 4;
@@ -1189,14 +1204,14 @@ hipError_t launch_gemv_routed(const void *w, const void *w2, const void *xq, con
     if (split) {
         switch (mt) {
             case 1: return launch_m<true, 1, JJO_RT_U1_SPLIT, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
-            case 2: return launch_m<true, 2, 2, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
-            default: return launch_m<true, 4, 4, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
+            case 2: return launch_m<true, 2, JJO_RT_U2_SPLIT, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
+            default: return launch_m<true, 4, JJO_RT_U4_SPLIT, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
         }
     }
     switch (mt) {
         case 1: return launch_m<false, 1, JJO_RT_U1_BLOCK, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
-        case 2: return launch_m<false, 2, 2, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
-        default: return launch_m<false, 4, kU4, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
+        case 2: return launch_m<false, 2, JJO_RT_U2_BLOCK, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
+        default: return launch_m<false, 4, JJO_RT_U4_BLOCK, false, true>(w, xq, nullptr, y, K, N, stream, ra, gy);
     }
 }
 
