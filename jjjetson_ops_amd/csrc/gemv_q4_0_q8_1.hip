@@ -1030,6 +1030,9 @@ constexpr int rg_for_s() {
 #ifndef JJO_RT_RG4_M1
 #define JJO_RT_RG4_M1 2
 #endif
+#ifndef JJO_RT_RG4_M2
+#define JJO_RT_RG4_M2 2  // four K slices, two-route chunks (E=8 top-2 T=8: 2-3%)
+#endif
 template <bool SPLIT, int M, int JS, bool FUSED, bool ROUTED>
 constexpr int rg_pick() {
     if (ROUTED && JS == 2 && M == 1 && JJO_RT_RG2_M1 > 0) return JJO_RT_RG2_M1;
@@ -1037,6 +1040,7 @@ constexpr int rg_pick() {
     if (ROUTED && JS == 3 && M == 1 && JJO_RT_RG3_M1 > 0) return JJO_RT_RG3_M1;
     if (ROUTED && JS == 3) return JJO_RT_RG3;
     if (ROUTED && JS == 4 && M == 1) return JJO_RT_RG4_M1;
+    if (ROUTED && JS == 4 && M == 2) return JJO_RT_RG4_M2;
     if (ROUTED && JS == 1 && M == 1 && JJO_RT_RG1_M1 > 0) return JJO_RT_RG1_M1;
     if (ROUTED && JS == 1 && M > 1 && JJO_RT_RG1_MX > 0) return JJO_RT_RG1_MX;
     if (ROUTED && JS == 4) return (!SPLIT && M == 4) ? JJO_RT_RG4_BLK_M4 : JJO_RT_RG4;
