@@ -1014,6 +1014,9 @@ constexpr int rg_for_s() {
 #ifndef JJO_RT_RG1_M1
 #define JJO_RT_RG1_M1 0  // one K slice, one route per chunk: 0 = the dense kernel's choice
 #endif
+#ifndef JJO_RT_RG1_M2
+#define JJO_RT_RG1_M2 0  // one K slice, two-route chunks: 0 = JJO_RT_RG1_MX
+#endif
 #ifndef JJO_RT_RG1_MX
 #define JJO_RT_RG1_MX 0  // one K slice, 2- and 4-route chunks: 0 = the dense kernel's choice
 #endif
@@ -1042,6 +1045,7 @@ constexpr int rg_pick() {
     if (ROUTED && JS == 4 && M == 1) return JJO_RT_RG4_M1;
     if (ROUTED && JS == 4 && M == 2) return JJO_RT_RG4_M2;
     if (ROUTED && JS == 1 && M == 1 && JJO_RT_RG1_M1 > 0) return JJO_RT_RG1_M1;
+    if (ROUTED && JS == 1 && M == 2 && JJO_RT_RG1_M2 > 0) return JJO_RT_RG1_M2;
     if (ROUTED && JS == 1 && M > 1 && JJO_RT_RG1_MX > 0) return JJO_RT_RG1_MX;
     if (ROUTED && JS == 4) return (!SPLIT && M == 4) ? JJO_RT_RG4_BLK_M4 : JJO_RT_RG4;
     return SPLIT ? rg_for_s<M, JS, FUSED>() : rg_for<M, JS, FUSED>();
